@@ -1,0 +1,186 @@
+"""Benchmark of the MI355X-native XTR-T5 Q4_K encoder (BASELINE.json metric).
+
+One step = one full encoder forward (embedding -> 12 blocks -> final norm -> 768->128
+projection + row norms) over one packed batch whose token ids are already resident in
+HBM.  Default workload: cfg2, 32 sequences padded to 256 with true lengths U[32, 256]
+(the reference runs them one at a time; here they are packed, so padding costs nothing).
+
+Prints ONE JSON line.  Extra fields:
+  roofline      -- the dominant kernel (batched FFN gate/up dequant-GEMM) vs f16 MFMA peak,
+                   timed with HIP events on the model's stream inside this process;
+  cpu_baseline  -- the CPU oracle (a C restatement of the reference's default t5-quantized
+                   CPU path: Q4_K dequantized to f32 at load, f32 GEMMs) on a bounded sample
+                   of the same workload, batch-1 per sequence as the reference runs it;
+  kernels       -- per-kernel-class averages from the same event timing.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "XTR-base Q4_K encoder tokens/sec (32×256) + dequant-GEMM % roofline"
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (n_seqs, min_len, max_len, padded_len, description)
+    "cfg2": (32, 32, 256, 256, "XTR-base Q4_K encoder, 32 seqs padded to 256, true lengths U[32,256]"),
+    "cfg3": (1, 32, 32, 32, "XTR-base Q4_K encoder, query regime: batch 1, 32 tokens"),
+    "cfg4": (256, 64, 512, 512, "XTR-base Q4_K encoder, bulk: 256 seqs padded to 512, lengths U[64,512]"),
+    "cfg5": (64, 16, 512, 512, "XTR-base hybrid layout (F32 q/k/v/o/wo, Q4_K FFN), 64 seqs padded to 512, U[16,512]"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_s: float) -> dict:
+    """Oracle (port of the reference CPU path) timed per sequence: 1 warmup + median of 7
+    (tools/t5-bench/src/main.rs:44-69), over as many sequences as fit the time budget."""
+    from oracle import oracle as orc
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    m = orc.OracleModel(img, cfg)
+    tok, secs, used = 0, 0.0, 0
+    t_start = time.perf_counter()
+    for b in range(cu.size - 1):
+        seq = ids[cu[b]:cu[b + 1]]
+        m.forward(seq, acc64=False)
+        times = []
+        for _ in range(7):
+            t = time.perf_counter()
+            m.forward(seq, acc64=False)
+            times.append(time.perf_counter() - t)
+        tok += seq.size
+        secs += sorted(times)[3]
+        used += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    m.close()
+    cpu = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": tok / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{used} of {cu.size - 1} sequences ({tok} tokens), batch-1 each, "
+                      f"median of 7 after 1 warmup; f32 dequantize-at-load path; CPU: {cpu}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU (got --gpus {args.gpus}); sequences are "
+              "independent, so N GPUs would each run this workload on their own share.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from witchcraft_amd import synth
+    from witchcraft_amd.encoder import T5EncoderModel
+
+    n_seqs, lo, hi, pad, desc = WORKLOADS[args.workload]
+    cfg = dict(synth.XTR_BASE)
+    t0 = time.perf_counter()
+    img = synth.make_model(cfg, seed=args.seed, layout="hybrid" if args.workload == "cfg5" else "q4k")
+    log(f"[bench] model built in {time.perf_counter() - t0:.1f}s ({len(img) / 1e6:.1f} MB GGUF)")
+    model = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
+    ids, cu = synth.ragged_batch(n_seqs, lo, hi, cfg["vocab_size"], seed=1000 + args.seed)
+    T = int(cu[-1])
+    dev = torch.device("cuda:0")
+    d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+    d_out = torch.empty((T, cfg["proj_dim"]), dtype=torch.float32, device=dev)
+    d_norm = torch.empty(T, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def step():
+        model.encode_device(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+
+    for _ in range(args.warmup):
+        step()
+    model.synchronize()
+    log(f"[bench] warmup done ({args.warmup} steps, T={T} tokens)")
+
+    # ---- timed region: whole-job throughput ----
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    model.synchronize()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    ms_per_step = elapsed / args.steps * 1e3
+    value = T * args.steps / elapsed
+    log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
+
+    # ---- per-kernel timing with HIP events on the model stream ----
+    model.set_profiling(True)
+    for _ in range(args.steps):
+        step()
+    model.synchronize()
+    stats = model.kernel_stats()
+    model.set_profiling(False)
+    kernels = {}
+    for name, s in stats.items():
+        if not s["launches"]:
+            continue
+        avg_ms = s["total_ms"] / s["launches"]
+        k = {"launches_per_step": s["launches"] / args.steps, "avg_us": avg_ms * 1e3,
+             "ms_per_step": s["total_ms"] / args.steps}
+        if s["flops"]:
+            k["tflops"] = s["flops"] / (s["total_ms"] * 1e-3) / 1e12
+            k["mfma_frac"] = k["tflops"] / PEAK_F16_TFLOPS
+        if s["bytes"]:
+            k["gbs"] = s["bytes"] / (s["total_ms"] * 1e-3) / 1e9
+            k["hbm_frac"] = k["gbs"] / PEAK_HBM_GBS
+        kernels[name] = k
+    dom = stats["gemm_ffn_gate_up"]
+    avg_s = dom["total_ms"] / dom["launches"] * 1e-3
+    flops_per_launch = dom["flops"] / dom["launches"]
+    achieved = flops_per_launch / avg_s / 1e12
+    roofline = {"kernel": "gemm_ffn_gate_up (wi_0|wi_1 Q4_K dequant-GEMM + gelu*up epilogue)",
+                "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
+                "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6}
+
+    base = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle port, bounded sample) ...")
+        base = cpu_baseline(img, cfg, ids, cu, args.cpu_budget)
+        log(f"[bench] CPU baseline {base['value']:.1f} tokens/s on {base['cores']} threads")
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {desc}", "global_batch": n_seqs, "seq_len": pad,
+                   "tokens_per_step": T, "weights": "random-init N(0,0.02^2), Q4_K (own quantizer)",
+                   "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": base, "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/*
+ * t5hip.h -- C ABI of the MI355X-native quantized XTR-T5 encoder (`t5-hip` backend).
+ *
+ * This is the drop-in boundary for Witchcraft's `t5_encoder` module alias
+ * (reference src/lib.rs:10-21).  Plain pointers and sizes only; every entry point
+ * returns 0 on success and a negative T5H_ERR_* code on failure, with a
+ * thread-local message from t5h_last_error().  Nothing here aborts or exits.
+ *
+ * Threading: a model handle is used by one thread at a time (the reference moves
+ * one T5EncoderModel into the napi indexer thread and guards another with a Mutex,
+ * src/napi.rs:293-304,483-551).  Handles share no mutable state; each owns its
+ * device buffers and its own HIP stream, so two handles may run concurrently.
+ */
+#ifndef T5HIP_H
+#define T5HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T5H_OK 0
+#define T5H_ERR_INVALID (-1)   /* bad argument (shape, id out of vocabulary, ...) */
+#define T5H_ERR_FORMAT (-2)    /* malformed GGUF / missing or mis-shaped tensor */
+#define T5H_ERR_HIP (-3)       /* HIP runtime failure */
+#define T5H_ERR_NOMEM (-4)     /* device or host allocation failed */
+#define T5H_ERR_NODEVICE (-5)  /* no usable gfx950 device */
+
+typedef struct t5h_model t5h_model;
+
+/* Model hyper-parameters.  Mirrors the fields of the reference `Config`
+ * (src/quantized_t5.rs:90-115) that the encoder reads; the host parses
+ * config.json into this struct (the reference does it with serde at :713-719). */
+typedef struct t5h_config {
+  int32_t vocab_size;                      /* Config::vocab_size */
+  int32_t d_model;                         /* Config::d_model (768) */
+  int32_t d_kv;                            /* Config::d_kv (64) */
+  int32_t d_ff;                            /* Config::d_ff (2048) */
+  int32_t num_layers;                      /* Config::num_layers (12) */
+  int32_t num_heads;                       /* Config::num_heads (12) */
+  int32_t relative_attention_num_buckets;  /* 32 */
+  int32_t relative_attention_max_distance; /* 128 (default, :64-66) */
+  float layer_norm_epsilon;                /* 1e-6 */
+  int32_t feed_forward_gated;              /* 1: "gated-gelu" (NewGelu), 0: "relu" */
+  int32_t proj_dim;                        /* rows of linear.weight (128, :690) */
+  int32_t max_seq_len;                     /* longest sequence accepted (embedder window 2048) */
+} t5h_config;
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* t5h_last_error(void);
+
+/* Fill `cfg` with XTR-base (T5-v1.1-base) values. */
+int t5h_config_xtr_base(t5h_config* cfg);
+
+/* Load an encoder from GGUF bytes (borrowed for the duration of the call).
+ * Replaces T5ModelBuilder::build_encoder + T5EncoderModel::load
+ * (src/quantized_t5.rs:681-696,731-749).  Linear weights may be Q4_K, F16 or F32
+ * (F16/F32 are kept as f16 on the device); the embedding table may be F32 or Q4_K.
+ * hip_device < 0 selects device 0. */
+int t5h_create(const void* gguf, size_t len, const t5h_config* cfg, int hip_device,
+               t5h_model** out);
+void t5h_destroy(t5h_model* model);
+
+/* Encode B packed sequences.  ids[T] holds the concatenated token ids of the
+ * sequences, cu_seqlens[B+1] their offsets (cu_seqlens[0] = 0, T = cu_seqlens[B]).
+ * Each sequence is encoded exactly as the reference encodes a [1, L] input
+ * (T5EncoderModel::forward, src/quantized_t5.rs:698-701): no token of one
+ * sequence attends to another.  out[T, proj_dim] receives the UN-normalised
+ * projections (host memory); out_norm[T] (optional, may be NULL) their L2 norms.
+ * Synchronous: returns after the results are in host memory, like the
+ * `.to_device(&Device::Cpu)` at src/embedder.rs:41. */
+int t5h_encode(t5h_model* model, const uint32_t* ids, const int32_t* cu_seqlens, int32_t B,
+               float* out, float* out_norm);
+
+/* As t5h_encode, but rows are L2-normalised (src/embedder.rs:7-9,94); norms are
+ * still reported pre-normalisation in out_norm when non-NULL. */
+int t5h_encode_normalized(t5h_model* model, const uint32_t* ids, const int32_t* cu_seqlens,
+                          int32_t B, float* out, float* out_norm);
+
+/* Device-resident variant for callers that keep ids and outputs in HBM.
+ * d_ids / d_out / d_norm are device pointers; cu_seqlens is a HOST array.
+ * Enqueued on the model's stream; returns without waiting (t5h_synchronize).
+ * Token ids >= vocab_size produce zero embeddings and raise the device error flag
+ * reported by t5h_synchronize. */
+int t5h_encode_device(t5h_model* model, const uint32_t* d_ids, const int32_t* cu_seqlens,
+                      int32_t B, float* d_out, float* d_norm);
+int t5h_synchronize(t5h_model* model);
+/* The model's hipStream_t (as void*), for event timing by the caller. */
+void* t5h_stream(t5h_model* model);
+
+/* Embedder::embed after tokenisation (src/embedder.rs:22-103): windows of
+ * max_len tokens overlapping by `stride`, summed; tokens whose pre-normalisation
+ * norm is < 1.0 dropped; rows L2-normalised.  out[n_tokens, proj_dim] receives the
+ * kept rows, kept_index[n_tokens] their token positions; *n_kept their count.
+ * Returns T5H_ERR_INVALID if every token is filtered (the reference bails). */
+int t5h_embed_ids(t5h_model* model, const uint32_t* ids, int32_t n_tokens, int32_t max_len,
+                  int32_t stride, float* out, int32_t* kept_index, int32_t* n_kept);
+
+/* ---- test hooks (teacher-forced parity checks) ---- */
+
+/* Q4_K -> f32, bit-exact with candle BlockQ4K::to_float (reached from
+ * src/quantized_t5.rs:44).  blocks/out are HOST buffers. */
+int t5h_q4k_dequant_f32(const void* blocks, size_t nblk, float* out, int hip_device);
+
+/* One T5Block (src/quantized_t5.rs:598-627) on packed sequences: x_in/x_out are
+ * host [T, d_model] f32. */
+int t5h_layer_forward(t5h_model* model, int32_t layer, const float* x_in,
+                      const int32_t* cu_seqlens, int32_t B, float* x_out);
+
+/* T5DenseGatedActDense::forward alone (src/quantized_t5.rs:231-252) on host x[T, d_model]:
+ * y = wo(gelu(x wi_0^T) * (x wi_1^T)).  mode 0: fused FFN kernel, 1: two-GEMM path. */
+int t5h_ffn_block(t5h_model* model, int32_t layer, const float* x, int32_t T, float* y,
+                  int32_t mode);
+
+/* Per-kernel timing with HIP events on the model stream (0 = off, 1 = on).
+ * t5h_kernel_stats fills up to `cap` records and returns the number of kernel
+ * classes; names are static strings. */
+typedef struct t5h_kernel_stat {
+  const char* name;
+  int64_t launches;
+  double total_ms;
+  double flops;  /* algorithmic FLOPs summed over launches (true tokens only) */
+  double bytes;  /* algorithmic HBM bytes summed over launches */
+} t5h_kernel_stat;
+int t5h_set_profiling(t5h_model* model, int32_t on);
+int t5h_kernel_stats(t5h_model* model, t5h_kernel_stat* stats, int32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,162 @@
+// k_misc.hip -- memory-bound kernels around the GEMMs: embedding gather, T5 RMSNorm,
+// row norms / L2 normalisation, window summation of the embedder.
+#include "common.hpp"
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Embedding gather (candle quantized_nn::Embedding, src/quantized_t5.rs:659,687):
+// x[t] = table[ids[t]].  The table is f32 or Q4_K (dequantized on the fly, bit-exact).
+// One wave per token.  Ids outside the vocabulary yield a zero row and set *err.
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ ids, int T,
+                                                    const void* __restrict__ table, int fmt, int vocab,
+                                                    int D, float* __restrict__ x, unsigned* err) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  const uint32_t id = ids[t];
+  float* xr = x + (size_t)t * D;
+  if (id >= (uint32_t)vocab) {
+    for (int i = lane; i < D; i += 64) xr[i] = 0.f;
+    if (lane == 0) atomicOr(err, 1u);
+    return;
+  }
+  if (fmt == EMB_F32) {
+    const float4* src = reinterpret_cast<const float4*>((const float*)table + (size_t)id * D);
+    for (int i = lane; i < D / 4; i += 64) reinterpret_cast<float4*>(xr)[i] = src[i];
+  } else {  // Q4_K table: D/256 blocks per row
+    const uint8_t* row = (const uint8_t*)table + (size_t)id * (D / QK_K) * Q4K_BYTES;
+    for (int e = lane; e < D; e += 64) {
+      const uint8_t* b = row + (e / QK_K) * Q4K_BYTES;
+      const int k = e % QK_K, c = k / 64, w = k % 64, hi = w >= 32, l = w & 31;
+      const int j = 2 * c + hi;
+      const uint8_t* s = b + 4;
+      int sc, m;
+      if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+      } else {
+        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+      }
+      const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+      const float dmin = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+      const uint8_t q = b[16 + 32 * c + l];
+      const float ds = d * (float)sc, mm = dmin * (float)m;
+      xr[e] = ds * (float)(hi ? (q >> 4) : (q & 15)) - mm;
+    }
+  }
+}
+
+// T5LayerNorm (src/quantized_t5.rs:162-173): x / sqrt(mean(x^2) + eps) * w, emitted as the
+// f16 GEMM operand.  One wave per row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w,
+                                                      _Float16* __restrict__ out, int T, int D,
+                                                      float eps) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
+  float ss = 0.f;
+  for (int i = lane; i < D / 4; i += 64) {
+    const float4 v = xr[i];
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  const float den = sqrtf(ss / (float)D + eps);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  h4* orow = reinterpret_cast<h4*>(out + (size_t)t * D);
+  for (int i = lane; i < D / 4; i += 64) {
+    const float4 v = xr[i], g = wr[i];
+    orow[i] = h4{(_Float16)((v.x / den) * g.x), (_Float16)((v.y / den) * g.y),
+                 (_Float16)((v.z / den) * g.z), (_Float16)((v.w / den) * g.w)};
+  }
+}
+
+// L2 norm of each output row (src/embedder.rs:83) and optional normalisation (:7-9).
+__global__ __launch_bounds__(256) void rownorm_kernel(float* __restrict__ y, float* __restrict__ norm,
+                                                      int T, int P, int normalize) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int lane = threadIdx.x & 63;
+  float* r = y + (size_t)t * P;
+  float ss = 0.f;
+  for (int i = lane; i < P; i += 64) ss += r[i] * r[i];
+  ss = wave_sum(ss);
+  const float n = sqrtf(ss);
+  if (lane == 0 && norm) norm[t] = n;
+  if (normalize)
+    for (int i = lane; i < P; i += 64) r[i] = r[i] / n;
+}
+
+__global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (_Float16)x[i];
+}
+
+// Embedder window summation (src/embedder.rs:38-63): token t's row is the sum, in window
+// order, of the rows src_rows[t*max_windows + w] (>= 0) of the per-window outputs.  Also
+// emits the pre-normalisation norm (:83) and the normalised row (:94).
+__global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict__ win,
+                                                         const int* __restrict__ src, int n, int maxw,
+                                                         int P, float* __restrict__ sum,
+                                                         float* __restrict__ norm,
+                                                         float* __restrict__ normalized) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= n) return;
+  const int lane = threadIdx.x & 63;
+  float ss = 0.f;
+  for (int i = lane; i < P; i += 64) {
+    float a = 0.f;
+    for (int w = 0; w < maxw; w++) {
+      const int r = src[t * maxw + w];
+      if (r >= 0) a += win[(size_t)r * P + i];
+    }
+    sum[(size_t)t * P + i] = a;
+    ss += a * a;
+  }
+  ss = wave_sum(ss);
+  const float nv = sqrtf(ss);
+  if (lane == 0) norm[t] = nv;
+  for (int i = lane; i < P; i += 64) normalized[(size_t)t * P + i] = sum[(size_t)t * P + i] / nv;
+}
+
+}  // namespace
+
+namespace t5k {
+hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
+                        float* x, unsigned* err, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err);
+  return hipGetLastError();
+}
+hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
+                          hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, out, T, D, eps);
+  return hipGetLastError();
+}
+hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize);
+  return hipGetLastError();
+}
+hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+hipError_t launch_window_sum(const float* win, const int* src, int n, int maxw, int P, float* sum,
+                             float* norm, float* normalized, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(window_sum_kernel, dim3((n + 3) / 4), dim3(256), 0, s, win, src, n, maxw, P, sum,
+                     norm, normalized);
+  return hipGetLastError();
+}
+}  // namespace t5k

@@ -1,0 +1,904 @@
+// t5hip_api.cpp -- the C ABI of include/t5hip.h: model load (GGUF -> HBM), workspace,
+// and the per-call launch sequence of the encoder on one HIP stream.
+//
+// Reference flow being replaced (src/quantized_t5.rs):
+//   T5EncoderModel::load :681-696   -> t5h_create
+//   T5Stack::forward     :654-670   -> enqueue_forward (embed, 12 blocks, final norm)
+//   T5EncoderModel::forward :698-701 -> + projection 768->128
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/t5hip.h"
+#include "common.hpp"
+#include "gguf.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIP_OK(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fail(T5H_ERR_HIP, std::string(#expr ": ") + hipGetErrorString(e_));       \
+  } while (0)
+
+struct Linear {
+  int N = 0, K = 0;
+  int fmt = WF_Q4K;
+  size_t off = 0;         // byte offset in the weight arena
+  const void* w = nullptr;  // device pointer (set after upload)
+  size_t bytes() const { return fmt == WF_Q4K ? (size_t)N * K / QK_K * Q4K_BYTES : (size_t)N * K * 2; }
+};
+
+struct Layer {
+  Linear qkv;           // fused [3*inner][D] when q, k, v share a format
+  Linear q, k, v;       // used when they do not
+  bool fused_qkv = true;
+  Linear o, wi0, wi1, wo;
+  size_t ln0_off = 0, ln1_off = 0;
+  const float *ln0 = nullptr, *ln1 = nullptr;
+};
+
+struct PendingTiming {
+  int kind;
+  hipEvent_t a, b;
+  double flops, bytes;
+};
+
+enum KernelKind {
+  K_EMBED, K_RMSNORM, K_GEMM_QKV, K_ATTN, K_GEMM_O, K_GEMM_GATE_UP, K_GEMM_WO, K_GEMM_PROJ,
+  K_ROWNORM, K_COUNT
+};
+const char* const kKernelNames[K_COUNT] = {
+    "embed_gather", "rmsnorm", "gemm_qkv", "attention", "gemm_o", "gemm_ffn_gate_up",
+    "gemm_ffn_wo", "gemm_proj", "rownorm"};
+
+struct StagingSlot {
+  void* host = nullptr;  // pinned
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool used = false;
+};
+
+}  // namespace
+
+struct t5h_model {
+  t5h_config cfg{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int inner = 0;
+
+  // ---- weights (one device arena) ----
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+  const void* emb = nullptr;
+  int emb_fmt = EMB_F32;
+  const float* rel_lut = nullptr;  // [H][2*maxl-1]
+  const float* final_ln = nullptr;
+  std::vector<Layer> layers;
+  Linear proj;
+
+  // ---- workspace ----
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  int cap_tokens = 0, cap_seqs = 0, cap_work = 0;
+  int tpad = 0;
+  float* x = nullptr;
+  _Float16* xn = nullptr;
+  _Float16* qkvb = nullptr;
+  _Float16* ao = nullptr;
+  _Float16* hb = nullptr;
+  float* out = nullptr;
+  float* norm = nullptr;
+  uint32_t* ids = nullptr;
+  int* cu = nullptr;
+  int2* work = nullptr;
+  unsigned* err_flag = nullptr;
+
+  // ---- host staging ----
+  StagingSlot slots[4];
+  int next_slot = 0;
+  void* io = nullptr;  // pinned buffer for synchronous calls
+  size_t io_cap = 0;
+
+  // ---- profiling ----
+  bool prof = false;
+  std::vector<PendingTiming> pending;
+  std::vector<hipEvent_t> event_pool;
+  t5h_kernel_stat stats[K_COUNT]{};
+
+  ~t5h_model() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& s : slots) {
+      if (s.host) (void)hipHostFree(s.host);
+      if (s.done) (void)hipEventDestroy(s.done);
+    }
+    if (io) (void)hipHostFree(io);
+    for (auto& p : pending) {
+      (void)hipEventDestroy(p.a);
+      (void)hipEventDestroy(p.b);
+    }
+    for (auto e : event_pool) (void)hipEventDestroy(e);
+    if (ws) (void)hipFree(ws);
+    if (arena) (void)hipFree(arena);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------------
+// Relative-position buckets (src/quantized_t5.rs:444-483).  Rust's f32::log(x, base) is
+// ln(x)/ln(base) on the platform logf; the table is built once on the host with the
+// same arithmetic and indexed on the device by the signed distance j - i.
+uint32_t rel_bucket(uint32_t i, uint32_t j, uint32_t nb_total, uint32_t max_distance) {
+  const uint32_t nb = nb_total / 2, max_exact = nb / 2;
+  if (i < j) {
+    if (j - i < max_exact) return j - i + nb;
+    const float b = logf((float)(j - i) / (float)max_exact) /
+                    logf((float)max_distance / (float)max_exact) * (float)(nb - max_exact);
+    return std::min(max_exact + nb + (uint32_t)b, nb_total - 1);
+  } else if (i - j < max_exact) {
+    return i - j;
+  } else {
+    const float b = logf((float)(i - j) / (float)max_exact) /
+                    logf((float)max_distance / (float)max_exact) * (float)(nb - max_exact);
+    return std::min(max_exact + (uint32_t)b, nb - 1);
+  }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int check_config(const t5h_config* c) {
+  if (!c) return fail(T5H_ERR_INVALID, "config is NULL");
+  if (c->vocab_size <= 0 || c->num_layers <= 0 || c->num_heads <= 0 || c->proj_dim <= 0 ||
+      c->max_seq_len <= 0 || c->relative_attention_num_buckets < 4 ||
+      c->relative_attention_max_distance <= 0)
+    return fail(T5H_ERR_INVALID, "config has non-positive dimensions");
+  if (c->d_kv != 64) return fail(T5H_ERR_INVALID, "d_kv must be 64 (attention kernel tile)");
+  const int inner = c->num_heads * c->d_kv;
+  if (c->d_model % 256 || c->d_ff % 256 || inner % 256)
+    return fail(T5H_ERR_INVALID, "d_model, d_ff and num_heads*d_kv must be multiples of 256");
+  if (c->proj_dim % 128) return fail(T5H_ERR_INVALID, "proj_dim must be a multiple of 128");
+  if (c->max_seq_len > 65536) return fail(T5H_ERR_INVALID, "max_seq_len too large");
+  return T5H_OK;
+}
+
+// Host-side weight collection before upload.
+struct HostArena {
+  std::vector<uint8_t> bytes;
+  size_t add(const void* src, size_t n) {
+    const size_t off = align256(bytes.size());
+    bytes.resize(off + n);
+    if (src) memcpy(bytes.data() + off, src, n);
+    return off;
+  }
+};
+
+// Adds a linear weight W[N][K]: Q4_K stays as raw blocks; F32/F16 become f16.
+int add_linear(HostArena& ha, const t5h::GgufFile& g, const std::string& name, int N, int K,
+               Linear& L) {
+  const t5h::GgufTensor* t = g.find(name);
+  if (!t) return fail(T5H_ERR_FORMAT, "missing tensor " + name);
+  if (t->shape.size() != 2 || (int)t->rows() != N || (int)t->cols() != K)
+    return fail(T5H_ERR_FORMAT, "tensor " + name + ": expected shape [" + std::to_string(N) + ", " +
+                                    std::to_string(K) + "]");
+  L.N = N;
+  L.K = K;
+  if (t->type == t5h::GGML_Q4_K) {
+    L.fmt = WF_Q4K;
+    L.off = ha.add(t->data, t->nbytes);
+  } else {
+    L.fmt = WF_F16;
+    L.off = ha.add(nullptr, (size_t)N * K * 2);
+    _Float16* dst = reinterpret_cast<_Float16*>(ha.bytes.data() + L.off);
+    const size_t ne = (size_t)N * K;
+    if (t->type == t5h::GGML_F32) {
+      const float* s = reinterpret_cast<const float*>(t->data);
+      for (size_t i = 0; i < ne; i++) dst[i] = (_Float16)s[i];
+    } else {
+      memcpy(dst, t->data, ne * 2);
+    }
+  }
+  return T5H_OK;
+}
+
+int add_f32_vector(HostArena& ha, const t5h::GgufFile& g, const std::string& name, size_t n,
+                   size_t& off) {
+  const t5h::GgufTensor* t = g.find(name);
+  if (!t) return fail(T5H_ERR_FORMAT, "missing tensor " + name);
+  uint64_t ne = 1;
+  for (auto d : t->shape) ne *= d;
+  if (ne != n) return fail(T5H_ERR_FORMAT, "tensor " + name + ": expected " + std::to_string(n) + " values");
+  off = ha.add(nullptr, n * 4);
+  float* dst = reinterpret_cast<float*>(ha.bytes.data() + off);
+  if (t->type == t5h::GGML_F32) {
+    memcpy(dst, t->data, n * 4);
+  } else if (t->type == t5h::GGML_F16) {
+    const _Float16* s = reinterpret_cast<const _Float16*>(t->data);
+    for (size_t i = 0; i < n; i++) dst[i] = (float)s[i];
+  } else {
+    return fail(T5H_ERR_FORMAT, "tensor " + name + ": expected F32 or F16");
+  }
+  return T5H_OK;
+}
+
+int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
+  if (T <= m->cap_tokens && B <= m->cap_seqs && nwork <= m->cap_work) return T5H_OK;
+  const int capT = std::max(T, m->cap_tokens), capB = std::max(B, m->cap_seqs);
+  const int capW = std::max(nwork, m->cap_work);
+  const int tpad = (capT + 127) / 128 * 128 + 128;
+  const t5h_config& c = m->cfg;
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off = align256(off + n);
+    return o;
+  };
+  const size_t o_x = take((size_t)tpad * c.d_model * 4);
+  const size_t o_xn = take((size_t)tpad * std::max(c.d_model, m->inner) * 2);
+  const size_t o_qkv = take((size_t)3 * tpad * m->inner * 2);
+  const size_t o_ao = take((size_t)tpad * m->inner * 2);
+  const size_t o_hb = take((size_t)tpad * c.d_ff * 2);
+  const size_t o_out = take((size_t)tpad * c.proj_dim * 4);
+  const size_t o_norm = take((size_t)tpad * 4);
+  const size_t o_ids = take((size_t)tpad * 4);
+  const size_t o_cu = take((size_t)(capB + 1) * 4);
+  const size_t o_work = take((size_t)capW * 8);
+  const size_t o_err = take(256);
+  if (m->ws) {
+    HIP_OK(hipStreamSynchronize(m->stream));
+    HIP_OK(hipFree(m->ws));
+    m->ws = nullptr;
+  }
+  if (hipMalloc(&m->ws, off) != hipSuccess) {
+    m->cap_tokens = m->cap_seqs = m->cap_work = 0;
+    return fail(T5H_ERR_NOMEM, "workspace allocation of " + std::to_string(off) + " bytes failed");
+  }
+  HIP_OK(hipMemset(m->ws, 0, off));
+  uint8_t* base = (uint8_t*)m->ws;
+  m->ws_bytes = off;
+  m->tpad = tpad;
+  m->x = (float*)(base + o_x);
+  m->xn = (_Float16*)(base + o_xn);
+  m->qkvb = (_Float16*)(base + o_qkv);
+  m->ao = (_Float16*)(base + o_ao);
+  m->hb = (_Float16*)(base + o_hb);
+  m->out = (float*)(base + o_out);
+  m->norm = (float*)(base + o_norm);
+  m->ids = (uint32_t*)(base + o_ids);
+  m->cu = (int*)(base + o_cu);
+  m->work = (int2*)(base + o_work);
+  m->err_flag = (unsigned*)(base + o_err);
+  m->cap_tokens = tpad - 128;
+  m->cap_seqs = capB;
+  m->cap_work = capW;
+  return T5H_OK;
+}
+
+int ensure_io(t5h_model* m, size_t bytes) {
+  if (bytes <= m->io_cap) return T5H_OK;
+  if (m->io) {
+    HIP_OK(hipStreamSynchronize(m->stream));
+    (void)hipHostFree(m->io);
+    m->io = nullptr;
+    m->io_cap = 0;
+  }
+  const size_t cap = std::max(bytes, (size_t)1 << 20);
+  if (hipHostMalloc(&m->io, cap, hipHostMallocDefault) != hipSuccess)
+    return fail(T5H_ERR_NOMEM, "pinned host allocation failed");
+  m->io_cap = cap;
+  return T5H_OK;
+}
+
+// Profiling brackets ----------------------------------------------------------------
+hipEvent_t take_event(t5h_model* m) {
+  if (!m->event_pool.empty()) {
+    hipEvent_t e = m->event_pool.back();
+    m->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+struct Timed {
+  t5h_model* m;
+  int kind;
+  double flops, bytes;
+  hipEvent_t a = nullptr;
+  Timed(t5h_model* m_, int k, double f, double b) : m(m_), kind(k), flops(f), bytes(b) {
+    if (m->prof) {
+      a = take_event(m);
+      (void)hipEventRecord(a, m->stream);
+    }
+  }
+  ~Timed() {
+    if (!m->prof || !a) return;
+    hipEvent_t b = take_event(m);
+    (void)hipEventRecord(b, m->stream);
+    m->pending.push_back({kind, a, b, flops, bytes});
+  }
+};
+
+void resolve_timings(t5h_model* m) {
+  for (auto& p : m->pending) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      t5h_kernel_stat& s = m->stats[p.kind];
+      s.launches++;
+      s.total_ms += ms;
+      s.flops += p.flops;
+      s.bytes += p.bytes;
+    }
+    m->event_pool.push_back(p.a);
+    m->event_pool.push_back(p.b);
+  }
+  m->pending.clear();
+}
+
+// Launch sequence -----------------------------------------------------------------
+int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, const _Float16* A, int lda,
+         int M, void* out, int ldo, int n_off = 0) {
+  GemmArgs a{};
+  a.A = A;
+  a.lda = lda;
+  a.W0 = W.w;
+  a.W1 = W1 ? W1->w : nullptr;
+  a.M = M;
+  a.N = W.N;
+  a.K = W.K;
+  a.out = out;
+  a.ldo = ldo;
+  a.n_off = n_off;
+  a.heads = m->cfg.num_heads;
+  a.dkv = m->cfg.d_kv;
+  a.tpad = m->tpad;
+  const double mats = W1 ? 2.0 : 1.0;
+  const double flops = 2.0 * M * W.N * W.K * mats;
+  const double out_bytes = (epi == EPI_F32 || epi == EPI_RESID ? 4.0 : 2.0) * M * W.N *
+                           (epi == EPI_RESID ? 2.0 : 1.0);
+  const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
+  Timed t(m, kind, flops, bytes);
+  HIP_OK(t5k::launch_gemm(epi, W.fmt, a, m->stream));
+  return T5H_OK;
+}
+
+// Uploads cu_seqlens and the attention work list through a pinned staging slot.
+int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
+  nwork = 0;
+  for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
+  StagingSlot& s = m->slots[m->next_slot];
+  m->next_slot = (m->next_slot + 1) % 4;
+  if (s.used) HIP_OK(hipEventSynchronize(s.done));
+  const size_t wofs = ((size_t)(B + 1) * 4 + 7) & ~(size_t)7;  // work list is 8-byte aligned
+  const size_t need = wofs + (size_t)nwork * 8;
+  if (need > s.cap) {
+    if (s.host) (void)hipHostFree(s.host);
+    s.host = nullptr;
+    s.cap = 0;
+    if (hipHostMalloc(&s.host, std::max(need, (size_t)4096), hipHostMallocDefault) != hipSuccess)
+      return fail(T5H_ERR_NOMEM, "pinned staging allocation failed");
+    s.cap = std::max(need, (size_t)4096);
+  }
+  if (!s.done) HIP_OK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+  int* hc = (int*)s.host;
+  memcpy(hc, cu, (size_t)(B + 1) * 4);
+  int2* hw = (int2*)((uint8_t*)s.host + wofs);
+  int w = 0;
+  for (int b = 0; b < B; b++) {
+    const int L = cu[b + 1] - cu[b];
+    for (int q = 0; q * 64 < L; q++) hw[w++] = make_int2(b, q);
+  }
+  HIP_OK(hipMemcpyAsync(m->cu, hc, (size_t)(B + 1) * 4, hipMemcpyHostToDevice, m->stream));
+  if (nwork) HIP_OK(hipMemcpyAsync(m->work, hw, (size_t)nwork * 8, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(hipEventRecord(s.done, m->stream));
+  s.used = true;
+  return T5H_OK;
+}
+
+int validate_cu(const t5h_model* m, const int32_t* cu, int B, int& T) {
+  if (B < 0 || (B > 0 && !cu)) return fail(T5H_ERR_INVALID, "bad batch description");
+  if (B == 0) {
+    T = 0;
+    return T5H_OK;
+  }
+  if (cu[0] != 0) return fail(T5H_ERR_INVALID, "cu_seqlens[0] must be 0");
+  for (int b = 0; b < B; b++) {
+    const int L = cu[b + 1] - cu[b];
+    if (L < 0) return fail(T5H_ERR_INVALID, "cu_seqlens must be non-decreasing");
+    if (L > m->cfg.max_seq_len)
+      return fail(T5H_ERR_INVALID, "sequence " + std::to_string(b) + " longer than max_seq_len");
+  }
+  T = cu[B];
+  return T5H_OK;
+}
+
+int run_block(t5h_model* m, int l, int T, int nwork) {
+  const t5h_config& c = m->cfg;
+  const Layer& Ly = m->layers[l];
+  const int D = c.d_model, inner = m->inner;
+  int rc;
+  {
+    Timed t(m, K_RMSNORM, 0, (double)T * D * 6);
+    HIP_OK(t5k::launch_rmsnorm(m->x, Ly.ln0, m->xn, T, D, c.layer_norm_epsilon, m->stream));
+  }
+  if (Ly.fused_qkv) {
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0))) return rc;
+  } else {
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner))) return rc;
+  }
+  {
+    AttnArgs a{};
+    a.qkv = m->qkvb;
+    a.out = m->ao;
+    a.cu = m->cu;
+    a.work = m->work;
+    a.lut = m->rel_lut;
+    a.heads = c.num_heads;
+    a.tpad = m->tpad;
+    a.maxl = c.max_seq_len;
+    Timed t(m, K_ATTN, 0, 0);
+    HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
+  }
+  if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D))) return rc;
+  {
+    Timed t(m, K_RMSNORM, 0, (double)T * D * 6);
+    HIP_OK(t5k::launch_rmsnorm(m->x, Ly.ln1, m->xn, T, D, c.layer_norm_epsilon, m->stream));
+  }
+  if (c.feed_forward_gated) {
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff))) return rc;
+  } else {
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff))) return rc;
+  }
+  if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, D))) return rc;
+  return T5H_OK;
+}
+
+// Attention FLOPs (QK^T + PV) of one block over the batch, true tokens only.
+double attn_flops(const t5h_model* m, const int32_t* cu, int B) {
+  double f = 0;
+  for (int b = 0; b < B; b++) {
+    const double L = cu[b + 1] - cu[b];
+    f += 4.0 * L * L * m->cfg.d_kv * m->cfg.num_heads;
+  }
+  return f;
+}
+
+// Full forward from device ids; results in m->out / m->norm (or the given pointers).
+int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
+                    float* d_norm, int normalize) {
+  int nwork = 0, rc;
+  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  if ((rc = upload_batch(m, cu, B, nwork))) return rc;
+  const t5h_config& c = m->cfg;
+  {
+    Timed t(m, K_EMBED, 0, (double)T * c.d_model * 8);
+    HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag,
+                             m->stream));
+  }
+  const size_t first_attn = m->pending.size();
+  for (int l = 0; l < c.num_layers; l++)
+    if ((rc = run_block(m, l, T, nwork))) return rc;
+  if (m->prof) {
+    const double af = attn_flops(m, cu, B);
+    for (size_t i = first_attn; i < m->pending.size(); i++)
+      if (m->pending[i].kind == K_ATTN) m->pending[i].flops = af;
+  }
+  {
+    Timed t(m, K_RMSNORM, 0, (double)T * c.d_model * 6);
+    HIP_OK(t5k::launch_rmsnorm(m->x, m->final_ln, m->xn, T, c.d_model, c.layer_norm_epsilon, m->stream));
+  }
+  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim)))
+    return rc;
+  {
+    Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
+    HIP_OK(t5k::launch_rownorm(d_out, d_norm, T, c.proj_dim, normalize, m->stream));
+  }
+  return T5H_OK;
+}
+
+int check_model(t5h_model* m) {
+  if (!m) return fail(T5H_ERR_INVALID, "model handle is NULL");
+  HIP_OK(hipSetDevice(m->device));
+  return T5H_OK;
+}
+
+int finish_sync(t5h_model* m) {
+  HIP_OK(hipStreamSynchronize(m->stream));
+  if (m->prof) resolve_timings(m);
+  unsigned flag = 0;
+  if (m->err_flag) {
+    HIP_OK(hipMemcpy(&flag, m->err_flag, 4, hipMemcpyDeviceToHost));
+    if (flag) {
+      HIP_OK(hipMemset(m->err_flag, 0, 4));
+      return fail(T5H_ERR_INVALID, "token id outside the vocabulary");
+    }
+  }
+  return T5H_OK;
+}
+
+int encode_host(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B, float* out,
+                float* out_norm, int normalize) {
+  int rc, T = 0;
+  if ((rc = check_model(m))) return rc;
+  if ((rc = validate_cu(m, cu, B, T))) return rc;
+  if (T == 0) return T5H_OK;
+  if (!ids || !out) return fail(T5H_ERR_INVALID, "ids/out must not be NULL");
+  for (int t = 0; t < T; t++)
+    if (ids[t] >= (uint32_t)m->cfg.vocab_size)
+      return fail(T5H_ERR_INVALID, "token id " + std::to_string(ids[t]) + " at position " +
+                                       std::to_string(t) + " outside the vocabulary");
+  const int P = m->cfg.proj_dim;
+  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  const size_t ids_b = align256((size_t)T * 4), out_b = (size_t)T * P * 4, norm_b = (size_t)T * 4;
+  if ((rc = ensure_io(m, ids_b + out_b + norm_b))) return rc;
+  uint8_t* io = (uint8_t*)m->io;
+  memcpy(io, ids, (size_t)T * 4);
+  HIP_OK(hipMemcpyAsync(m->ids, io, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
+  if ((rc = enqueue_forward(m, m->ids, cu, B, T, m->out, m->norm, normalize))) return rc;
+  HIP_OK(hipMemcpyAsync(io + ids_b, m->out, out_b, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(io + ids_b + out_b, m->norm, norm_b, hipMemcpyDeviceToHost, m->stream));
+  if ((rc = finish_sync(m))) return rc;
+  memcpy(out, io + ids_b, out_b);
+  if (out_norm) memcpy(out_norm, io + ids_b + out_b, norm_b);
+  return T5H_OK;
+}
+
+int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_device, t5h_model** out) {
+  if (!out) return fail(T5H_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  int rc;
+  if ((rc = check_config(cfg))) return rc;
+  if (!gguf || len == 0) return fail(T5H_ERR_FORMAT, "model GGUF bytes are missing");
+  t5h::GgufFile g;
+  std::string perr;
+  if (!t5h::parse_gguf((const uint8_t*)gguf, len, g, perr)) return fail(T5H_ERR_FORMAT, perr);
+
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(T5H_ERR_NODEVICE, "no HIP device");
+  const int dev = hip_device < 0 ? 0 : hip_device;
+  if (dev >= ndev) return fail(T5H_ERR_NODEVICE, "HIP device index out of range");
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, dev));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(T5H_ERR_NODEVICE, std::string("t5-hip kernels target gfx950, device is ") + prop.gcnArchName);
+  HIP_OK(hipSetDevice(dev));
+
+  std::unique_ptr<t5h_model> m(new t5h_model());
+  m->cfg = *cfg;
+  m->device = dev;
+  m->inner = cfg->num_heads * cfg->d_kv;
+  const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
+
+  HostArena ha;
+  // Embedding table: encoder.embed_tokens or shared (src/quantized_t5.rs:682-687).
+  const char* emb_name = g.find("shared.weight") ? "shared.weight" : "encoder.embed_tokens.weight";
+  const t5h::GgufTensor* et = g.find(emb_name);
+  if (!et) return fail(T5H_ERR_FORMAT, "missing tensor encoder.embed_tokens.weight");
+  if (et->shape.size() != 2 || (int)et->rows() != cfg->vocab_size || (int)et->cols() != D)
+    return fail(T5H_ERR_FORMAT, std::string("tensor ") + emb_name + ": expected [vocab_size, d_model]");
+  size_t emb_off;
+  if (et->type == t5h::GGML_Q4_K) {
+    m->emb_fmt = EMB_Q4K;
+    emb_off = ha.add(et->data, et->nbytes);
+  } else {
+    m->emb_fmt = EMB_F32;
+    emb_off = ha.add(nullptr, (size_t)cfg->vocab_size * D * 4);
+    float* dst = reinterpret_cast<float*>(ha.bytes.data() + emb_off);
+    if (et->type == t5h::GGML_F32)
+      memcpy(dst, et->data, et->nbytes);
+    else
+      for (size_t i = 0; i < (size_t)cfg->vocab_size * D; i++) dst[i] = (float)((const _Float16*)et->data)[i];
+  }
+  // Relative attention bias of block 0 (src/quantized_t5.rs:351-360,640) -> LUT by j - i.
+  const std::string rb_name = "encoder.block.0.layer.0.SelfAttention.relative_attention_bias.weight";
+  const t5h::GgufTensor* rb = g.find(rb_name);
+  if (!rb) return fail(T5H_ERR_FORMAT, "missing tensor " + rb_name);
+  if (rb->type != t5h::GGML_F32 || rb->shape.size() != 2 ||
+      (int)rb->rows() != cfg->relative_attention_num_buckets || (int)rb->cols() != H)
+    return fail(T5H_ERR_FORMAT, "tensor " + rb_name + ": expected F32 [num_buckets, num_heads]");
+  const int maxl = cfg->max_seq_len, span = 2 * maxl - 1;
+  const size_t lut_off = ha.add(nullptr, (size_t)H * span * 4);
+  {
+    float* lut = reinterpret_cast<float*>(ha.bytes.data() + lut_off);
+    const float* tab = reinterpret_cast<const float*>(rb->data);
+    for (int dlt = -(maxl - 1); dlt <= maxl - 1; dlt++) {
+      const uint32_t i = dlt < 0 ? (uint32_t)(-dlt) : 0u, j = dlt < 0 ? 0u : (uint32_t)dlt;
+      const uint32_t b = rel_bucket(i, j, cfg->relative_attention_num_buckets,
+                                    cfg->relative_attention_max_distance);
+      for (int h = 0; h < H; h++) lut[(size_t)h * span + dlt + maxl - 1] = tab[b * H + h];
+    }
+  }
+  m->layers.resize(cfg->num_layers);
+  for (int l = 0; l < cfg->num_layers; l++) {
+    Layer& Ly = m->layers[l];
+    const std::string p = "encoder.block." + std::to_string(l) + ".layer.";
+    if ((rc = add_f32_vector(ha, g, p + "0.layer_norm.weight", D, Ly.ln0_off))) return rc;
+    if ((rc = add_f32_vector(ha, g, p + "1.layer_norm.weight", D, Ly.ln1_off))) return rc;
+    // q, k, v: fused into one [3*inner, D] operand when they share a storage format
+    // (the hybrid path fuses them the same way, src/quantized_t5.rs:321-339).
+    const t5h::GgufTensor* tq = g.find(p + "0.SelfAttention.q.weight");
+    const t5h::GgufTensor* tk = g.find(p + "0.SelfAttention.k.weight");
+    const t5h::GgufTensor* tv = g.find(p + "0.SelfAttention.v.weight");
+    if (!tq || !tk || !tv) return fail(T5H_ERR_FORMAT, "missing q/k/v weights in block " + std::to_string(l));
+    auto kind = [](const t5h::GgufTensor* t) { return t->type == t5h::GGML_Q4_K ? 0 : 1; };
+    Ly.fused_qkv = kind(tq) == kind(tk) && kind(tk) == kind(tv);
+    if ((rc = add_linear(ha, g, p + "0.SelfAttention.q.weight", inner, D, Ly.q))) return rc;
+    if ((rc = add_linear(ha, g, p + "0.SelfAttention.k.weight", inner, D, Ly.k))) return rc;
+    if ((rc = add_linear(ha, g, p + "0.SelfAttention.v.weight", inner, D, Ly.v))) return rc;
+    if (Ly.fused_qkv) {
+      // the three regions are consecutive: re-pack them contiguously
+      Ly.qkv.N = 3 * inner;
+      Ly.qkv.K = D;
+      Ly.qkv.fmt = Ly.q.fmt;
+      const size_t one = Ly.q.bytes();
+      std::vector<uint8_t> tmp(3 * one);
+      memcpy(tmp.data(), ha.bytes.data() + Ly.q.off, one);
+      memcpy(tmp.data() + one, ha.bytes.data() + Ly.k.off, one);
+      memcpy(tmp.data() + 2 * one, ha.bytes.data() + Ly.v.off, one);
+      Ly.qkv.off = ha.add(tmp.data(), tmp.size());
+    }
+    if ((rc = add_linear(ha, g, p + "0.SelfAttention.o.weight", D, inner, Ly.o))) return rc;
+    if (cfg->feed_forward_gated) {
+      if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi_0.weight", F, D, Ly.wi0))) return rc;
+      if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi_1.weight", F, D, Ly.wi1))) return rc;
+      if (Ly.wi0.fmt != Ly.wi1.fmt) return fail(T5H_ERR_FORMAT, "wi_0 and wi_1 must share a storage format");
+    } else {
+      if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi.weight", F, D, Ly.wi0))) return rc;
+    }
+    if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wo.weight", D, F, Ly.wo))) return rc;
+  }
+  size_t fln_off;
+  if ((rc = add_f32_vector(ha, g, "encoder.final_layer_norm.weight", D, fln_off))) return rc;
+  if ((rc = add_linear(ha, g, "linear.weight", cfg->proj_dim, D, m->proj))) return rc;
+
+  // ---- upload ----
+  m->arena_bytes = align256(ha.bytes.size());
+  if (hipMalloc(&m->arena, m->arena_bytes) != hipSuccess)
+    return fail(T5H_ERR_NOMEM, "weight allocation of " + std::to_string(m->arena_bytes) + " bytes failed");
+  HIP_OK(hipMemcpy(m->arena, ha.bytes.data(), ha.bytes.size(), hipMemcpyHostToDevice));
+  uint8_t* base = (uint8_t*)m->arena;
+  auto bind = [&](Linear& L) { L.w = base + L.off; };
+  m->emb = base + emb_off;
+  m->rel_lut = (const float*)(base + lut_off);
+  m->final_ln = (const float*)(base + fln_off);
+  for (auto& Ly : m->layers) {
+    Ly.ln0 = (const float*)(base + Ly.ln0_off);
+    Ly.ln1 = (const float*)(base + Ly.ln1_off);
+    bind(Ly.q); bind(Ly.k); bind(Ly.v); bind(Ly.o); bind(Ly.wi0); bind(Ly.wo);
+    if (cfg->feed_forward_gated) bind(Ly.wi1);
+    if (Ly.fused_qkv) bind(Ly.qkv);
+  }
+  bind(m->proj);
+  HIP_OK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  for (int k = 0; k < K_COUNT; k++) m->stats[k].name = kKernelNames[k];
+  *out = m.release();
+  g_err.clear();
+  return T5H_OK;
+}
+
+}  // namespace
+
+// =================================================================================
+extern "C" {
+
+const char* t5h_last_error(void) { return g_err.c_str(); }
+
+int t5h_config_xtr_base(t5h_config* c) {
+  if (!c) return fail(T5H_ERR_INVALID, "config is NULL");
+  c->vocab_size = 32128;
+  c->d_model = 768;
+  c->d_kv = 64;
+  c->d_ff = 2048;
+  c->num_layers = 12;
+  c->num_heads = 12;
+  c->relative_attention_num_buckets = 32;
+  c->relative_attention_max_distance = 128;
+  c->layer_norm_epsilon = 1e-6f;
+  c->feed_forward_gated = 1;
+  c->proj_dim = 128;
+  c->max_seq_len = 2048;
+  return T5H_OK;
+}
+
+int t5h_create(const void* gguf, size_t len, const t5h_config* cfg, int hip_device, t5h_model** out) {
+  try {
+    return create_impl(gguf, len, cfg, hip_device, out);
+  } catch (const std::bad_alloc&) {
+    return fail(T5H_ERR_NOMEM, "host allocation failed while loading the model");
+  }
+}
+
+void t5h_destroy(t5h_model* model) {
+  if (!model) return;
+  (void)hipSetDevice(model->device);
+  delete model;
+}
+
+int t5h_encode(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B, float* out, float* out_norm) {
+  return encode_host(m, ids, cu, B, out, out_norm, 0);
+}
+
+int t5h_encode_normalized(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B, float* out,
+                          float* out_norm) {
+  return encode_host(m, ids, cu, B, out, out_norm, 1);
+}
+
+int t5h_encode_device(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int32_t B, float* d_out,
+                      float* d_norm) {
+  int rc, T = 0;
+  if ((rc = check_model(m))) return rc;
+  if ((rc = validate_cu(m, cu, B, T))) return rc;
+  if (T == 0) return T5H_OK;
+  if (!d_ids || !d_out) return fail(T5H_ERR_INVALID, "d_ids/d_out must not be NULL");
+  return enqueue_forward(m, d_ids, cu, B, T, d_out, d_norm, 0);
+}
+
+int t5h_synchronize(t5h_model* m) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  return finish_sync(m);
+}
+
+void* t5h_stream(t5h_model* m) { return m ? (void*)m->stream : nullptr; }
+
+int t5h_embed_ids(t5h_model* m, const uint32_t* ids, int32_t n, int32_t max_len, int32_t stride,
+                  float* out, int32_t* kept_index, int32_t* n_kept) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  if (!ids || !out || !kept_index || !n_kept || n <= 0)
+    return fail(T5H_ERR_INVALID, "embed_ids: bad arguments");
+  if (max_len <= 0 || max_len > m->cfg.max_seq_len || stride < 0 || stride >= max_len)
+    return fail(T5H_ERR_INVALID, "embed_ids: need 0 < max_len <= max_seq_len and 0 <= stride < max_len");
+  // Windows of src/embedder.rs:38-63.
+  std::vector<int> wstart, wend;
+  for (int start = 0;;) {
+    const int end = std::min(start + max_len, n);
+    wstart.push_back(start);
+    wend.push_back(end);
+    if (end == n) break;
+    start = end > stride ? end - stride : 0;
+  }
+  const int W = (int)wstart.size();
+  std::vector<int32_t> cu(W + 1, 0);
+  std::vector<uint32_t> wids;
+  for (int w = 0; w < W; w++) {
+    cu[w + 1] = cu[w] + (wend[w] - wstart[w]);
+    wids.insert(wids.end(), ids + wstart[w], ids + wend[w]);
+  }
+  std::vector<int> cover(n, 0);
+  int maxw = 1;
+  for (int w = 0; w < W; w++)
+    for (int t = wstart[w]; t < wend[w]; t++) maxw = std::max(maxw, ++cover[t]);
+  std::vector<int> src((size_t)n * maxw, -1);
+  std::fill(cover.begin(), cover.end(), 0);
+  for (int w = 0; w < W; w++)
+    for (int t = wstart[w]; t < wend[w]; t++) src[(size_t)t * maxw + cover[t]++] = cu[w] + (t - wstart[w]);
+  const int P = m->cfg.proj_dim, T = cu[W];
+  std::vector<float> win((size_t)T * P);
+  if ((rc = encode_host(m, wids.data(), cu.data(), W, win.data(), nullptr, 0))) return rc;
+  // Window sum + norms + normalisation on the device.
+  float* d_buf = nullptr;
+  const size_t need = (size_t)T * P * 4 + (size_t)n * maxw * 4 + (size_t)n * P * 8 + (size_t)n * 4 + 1024;
+  HIP_OK(hipMalloc(&d_buf, need));
+  std::unique_ptr<void, void (*)(void*)> guard(d_buf, [](void* p) { (void)hipFree(p); });
+  float* d_win = d_buf;
+  int* d_src = (int*)(d_win + (size_t)T * P);
+  float* d_sum = (float*)(d_src + (size_t)n * maxw);
+  float* d_nrm = d_sum + (size_t)n * P;
+  float* d_nz = d_nrm + n;
+  HIP_OK(hipMemcpyAsync(d_win, win.data(), (size_t)T * P * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(hipMemcpyAsync(d_src, src.data(), src.size() * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(t5k::launch_window_sum(d_win, d_src, n, maxw, P, d_sum, d_nrm, d_nz, m->stream));
+  std::vector<float> nz((size_t)n * P), nrm(n);
+  HIP_OK(hipMemcpyAsync(nz.data(), d_nz, nz.size() * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(nrm.data(), d_nrm, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipStreamSynchronize(m->stream));
+  int k = 0;
+  for (int t = 0; t < n; t++) {
+    if (nrm[t] >= 1.0f) {  // MIN_NORM, src/embedder.rs:79-88
+      memcpy(out + (size_t)k * P, nz.data() + (size_t)t * P, (size_t)P * 4);
+      kept_index[k++] = t;
+    }
+  }
+  *n_kept = k;
+  if (k == 0) return fail(T5H_ERR_INVALID, "all token embeddings below minimum norm threshold");
+  return T5H_OK;
+}
+
+int t5h_q4k_dequant_f32(const void* blocks, size_t nblk, float* out, int hip_device) {
+  if (nblk == 0) return T5H_OK;
+  if (!blocks || !out) return fail(T5H_ERR_INVALID, "NULL buffer");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(T5H_ERR_NODEVICE, "no HIP device");
+  HIP_OK(hipSetDevice(hip_device < 0 ? 0 : hip_device));
+  void* d_in = nullptr;
+  float* d_out = nullptr;
+  HIP_OK(hipMalloc(&d_in, nblk * Q4K_BYTES));
+  std::unique_ptr<void, void (*)(void*)> g1(d_in, [](void* p) { (void)hipFree(p); });
+  HIP_OK(hipMalloc((void**)&d_out, nblk * QK_K * 4));
+  std::unique_ptr<void, void (*)(void*)> g2(d_out, [](void* p) { (void)hipFree(p); });
+  HIP_OK(hipMemcpy(d_in, blocks, nblk * Q4K_BYTES, hipMemcpyHostToDevice));
+  HIP_OK(t5k::launch_q4k_dequant(d_in, nblk, d_out, nullptr));
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(out, d_out, nblk * QK_K * 4, hipMemcpyDeviceToHost));
+  return T5H_OK;
+}
+
+int t5h_layer_forward(t5h_model* m, int32_t layer, const float* x_in, const int32_t* cu, int32_t B,
+                      float* x_out) {
+  int rc, T = 0;
+  if ((rc = check_model(m))) return rc;
+  if (layer < 0 || layer >= m->cfg.num_layers) return fail(T5H_ERR_INVALID, "layer index out of range");
+  if ((rc = validate_cu(m, cu, B, T))) return rc;
+  if (T == 0) return T5H_OK;
+  if (!x_in || !x_out) return fail(T5H_ERR_INVALID, "NULL buffer");
+  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  int nwork = 0;
+  if ((rc = upload_batch(m, cu, B, nwork))) return rc;
+  const size_t bytes = (size_t)T * m->cfg.d_model * 4;
+  HIP_OK(hipMemcpyAsync(m->x, x_in, bytes, hipMemcpyHostToDevice, m->stream));
+  if ((rc = run_block(m, layer, T, nwork))) return rc;
+  HIP_OK(hipMemcpyAsync(x_out, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
+  return finish_sync(m);
+}
+
+int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float* y, int32_t mode) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  if (layer < 0 || layer >= m->cfg.num_layers) return fail(T5H_ERR_INVALID, "layer index out of range");
+  if (T <= 0 || !x || !y) return fail(T5H_ERR_INVALID, "bad FFN block arguments");
+  if (mode != 0 && mode != 1) return fail(T5H_ERR_INVALID, "mode must be 0 or 1");
+  if (!m->cfg.feed_forward_gated) return fail(T5H_ERR_INVALID, "model FFN is not gated");
+  if ((rc = ensure_workspace(m, T, 1, (T + 63) / 64 + 1))) return rc;
+  const t5h_config& c = m->cfg;
+  const Layer& Ly = m->layers[layer];
+  const size_t bytes = (size_t)T * c.d_model * 4;
+  HIP_OK(hipMemcpyAsync(m->x, x, bytes, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(t5k::launch_f32_to_f16(m->x, m->xn, (size_t)T * c.d_model, m->stream));
+  if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, c.d_model, T, m->hb, c.d_ff))) return rc;
+  if ((rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, c.d_model))) return rc;
+  HIP_OK(hipMemcpyAsync(y, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
+  return finish_sync(m);
+}
+
+int t5h_set_profiling(t5h_model* m, int32_t on) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  HIP_OK(hipStreamSynchronize(m->stream));
+  resolve_timings(m);
+  m->prof = on != 0;
+  for (int k = 0; k < K_COUNT; k++) {
+    m->stats[k].launches = 0;
+    m->stats[k].total_ms = m->stats[k].flops = m->stats[k].bytes = 0;
+  }
+  return T5H_OK;
+}
+
+int t5h_kernel_stats(t5h_model* m, t5h_kernel_stat* stats, int32_t cap) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  HIP_OK(hipStreamSynchronize(m->stream));
+  resolve_timings(m);
+  for (int k = 0; k < K_COUNT && k < cap; k++) stats[k] = m->stats[k];
+  return K_COUNT;
+}
+
+}  // extern "C"
