@@ -61,14 +61,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
 __device__ __forceinline__ float gelu_tanh_dev(float x) {
   const float u = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
   const float e = __expf(2.0f * u);
-  const float t = 1.0f - 2.0f / (e + 1.0f);
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
   return 0.5f * x * (1.0f + t);
 }
 
 // Host-side launchers (defined in the .hip files) --------------------------------
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
-hipError_t launch_gemm(int epi, int wfmt, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm(int epi, int wfmt, int mw, const GemmArgs& a, hipStream_t s);
+int gemm_pick_mw(int M, int n_tiles, int cus);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
                         float* x, unsigned* err_flag, hipStream_t s);

@@ -4,217 +4,250 @@
 // super-blocks (or f16).  Reference: every linear of the encoder, candle QMatMul /
 // f32 matmul (src/quantized_t5.rs:383-424 QKV, :501 O, :231-252 FFN, :700 projection).
 //
-// Workgroup: 256 threads = 4 wave64s in a 2x2 grid, tile BM=128 x BN=128 x BK=64.
-// Each wave owns a 64x64 sub-tile = 4x4 MFMA 16x16 blocks (64 f32 accumulators/lane).
-// Per K step of 64 the workgroup:
-//   - reads the A tile (128 rows x 128 B f16) with 16-byte coalesced loads,
-//   - reads for each of its 128 weight rows the 16-byte Q4_K header (d, dmin, scales)
-//     and 32 bytes of packed nibbles (one 64-value chunk = sub-blocks 2c and 2c+1),
-//   - dequantizes nibbles to f16 (f32 scale/min math, then one rounding) into LDS,
-//   - runs 2 x 16 MFMAs per wave out of LDS.
-// Global loads for step k+1 are issued before the MFMAs of step k (register double
-// buffer) and the LDS tiles are double-buffered, so one barrier per step suffices.
+// Workgroup = MW wave64s stacked along M; tile BM = 64*MW tokens x BN = 128 weight rows,
+// K stepped by 64 (one Q4_K chunk: sub-blocks 2c and 2c+1 of every row).
+//  * B (weights): each K step the workgroup reads, per weight row, the 16-byte Q4_K header
+//    (d, dmin, 12 scale bytes) and 32 bytes of packed nibbles, dequantizes them with f32
+//    scale/min math (one rounding to f16 per value) and stores the 128x64 f16 tile in LDS,
+//    double-buffered.  Every wave consumes the whole tile, so the dequantization is
+//    amortised over BM tokens.
+//  * A (activations): each wave owns 64 rows and streams them straight from global memory
+//    into VGPRs -- no LDS round trip.  A lane of lane-group g reads 32 contiguous bytes
+//    (K = 16g .. 16g+15) of its row, so the 4 lane groups cover one 128-byte line per row.
+//    MFMA step s (of 2) uses K = 16g + 8s + 0..7; the B fragments are read from LDS with
+//    the same K order, so the product is the plain dot product.
+//  * Each wave holds 64 x 128 f32 accumulators (4 x 8 blocks of 16x16).
+//  * Tiles are ordered so that each XCD (8 per device, workgroups dealt round-robin) works
+//    on a contiguous band of M tiles: its L2 holds the A rows it streams plus the weights.
 #include "common.hpp"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, LDSK = BK + 8;  // +16 B row pad vs bank conflicts
+constexpr int BN = 128, BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 reads
 
-__device__ __forceinline__ void scale_min_u32(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc,
-                                              int& m) {
-  // scales[12] packed in three little-endian dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11).
-  auto byte = [&](int i) -> int {
-    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-    return (int)((w >> (8 * (i & 3))) & 0xff);
-  };
-  if (j < 4) {
-    sc = byte(j) & 63;
-    m = byte(j + 4) & 63;
-  } else {
-    sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
-    m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
-  }
+__device__ __forceinline__ int sbyte(const uint4& hd, int i) {
+  // byte i (0..11) of the 12 packed scale bytes = header bytes 4..15
+  const uint32_t w = i < 4 ? hd.y : (i < 8 ? hd.z : hd.w);
+  return (int)((w >> (8 * (i & 3))) & 0xff);
 }
 
-// Map a B-tile row to (weight matrix, output column).  For the gated epilogue the
-// 128 tile rows interleave W0 and W1 so that each wave holds the gate and the up
-// projection of the same 32 columns: wave column wn covers tile rows [64wn, 64wn+64),
-// MFMA blocks ni=0,1 are W0 columns and ni=2,3 the same W1 columns.
-template <int EPI>
-__device__ __forceinline__ void brow_map(int r, int n0, int& mat, int& n) {
-  if (EPI == EPI_GATED) {
-    const int wn = r >> 6, ni = (r >> 4) & 3, c = r & 15;
-    mat = ni >> 1;
-    n = n0 + wn * 32 + (ni & 1) * 16 + c;
+// GGML get_scale_min_k4 for the chunk pair (2c, 2c+1); c is wave-uniform.
+__device__ __forceinline__ void chunk_scales(const uint4& hd, int c, float& s0, float& o0, float& s1,
+                                             float& o1) {
+  const float d = f16_bits_to_f32(hd.x & 0xffff), dmin = f16_bits_to_f32(hd.x >> 16);
+  int sc0, m0, sc1, m1;
+  const int j0 = 2 * c, j1 = 2 * c + 1;
+  if (c < 2) {
+    sc0 = sbyte(hd, j0) & 63;
+    m0 = sbyte(hd, j0 + 4) & 63;
+    sc1 = sbyte(hd, j1) & 63;
+    m1 = sbyte(hd, j1 + 4) & 63;
   } else {
-    mat = 0;
+    sc0 = (sbyte(hd, j0 + 4) & 15) | ((sbyte(hd, j0 - 4) >> 6) << 4);
+    m0 = (sbyte(hd, j0 + 4) >> 4) | ((sbyte(hd, j0) >> 6) << 4);
+    sc1 = (sbyte(hd, j1 + 4) & 15) | ((sbyte(hd, j1 - 4) >> 6) << 4);
+    m1 = (sbyte(hd, j1 + 4) >> 4) | ((sbyte(hd, j1) >> 6) << 4);
+  }
+  s0 = d * (float)sc0;
+  o0 = dmin * (float)m0;
+  s1 = d * (float)sc1;
+  o1 = dmin * (float)m1;
+}
+
+// Dequantize 4 packed bytes (8 nibbles) -> 4 low-nibble and 4 high-nibble f16 values.
+__device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, float o1, h4& lo, h4& hi) {
+  const uint32_t l = v & 0x0f0f0f0fu, h = (v >> 4) & 0x0f0f0f0fu;
+  lo = h4{(_Float16)(s0 * (float)(l & 0xff) - o0), (_Float16)(s0 * (float)((l >> 8) & 0xff) - o0),
+          (_Float16)(s0 * (float)((l >> 16) & 0xff) - o0), (_Float16)(s0 * (float)(l >> 24) - o0)};
+  hi = h4{(_Float16)(s1 * (float)(h & 0xff) - o1), (_Float16)(s1 * (float)((h >> 8) & 0xff) - o1),
+          (_Float16)(s1 * (float)((h >> 16) & 0xff) - o1), (_Float16)(s1 * (float)(h >> 24) - o1)};
+}
+
+template <int EPI>
+__device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const void*& W, int& n) {
+  if (EPI == EPI_GATED) {  // rows [0,64): W0 columns n0.., rows [64,128): W1 same columns
+    W = r < 64 ? p.W0 : p.W1;
+    n = n0 + (r & 63);
+  } else {
+    W = p.W0;
     n = n0 + r;
   }
 }
 
-template <int EPI, int WF>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDSK];
+// Raw B data of one K step held in registers between the global load and the LDS store.
+template <int WF, int NT>
+struct BRaw {
+  static constexpr int TPR = NT / BN;           // threads per weight row (Q4_K)
+  static constexpr int BPT = 32 / TPR;          // nibble bytes per thread
+  static constexpr int F16_LOADS = BN * BK * 2 / 16 / NT;
+  uint4 hd;
+  uint32_t q[BPT / 4];
+  uint4 f[WF == WF_F16 ? F16_LOADS : 1];
+};
+
+template <int EPI, int WF, int NT>
+__device__ __forceinline__ void load_b(BRaw<WF, NT>& br, const GemmArgs& p, int n0, int kt, int tid) {
+  using R = BRaw<WF, NT>;
+  if (WF == WF_Q4K) {
+    const int r = tid / R::TPR, part = tid % R::TPR;
+    const void* W;
+    int n;
+    brow<EPI>(r, n0, p, W, n);
+    const int kb = (kt * BK) / QK_K, c = ((kt * BK) % QK_K) / 64;
+    const uint8_t* blk = (const uint8_t*)W + ((size_t)n * (p.K / QK_K) + kb) * Q4K_BYTES;
+    br.hd = *reinterpret_cast<const uint4*>(blk);
+    const uint8_t* qs = blk + 16 + 32 * c + part * R::BPT;
+    if constexpr (R::BPT == 32) {
+      const uint4 a = *reinterpret_cast<const uint4*>(qs), b = *reinterpret_cast<const uint4*>(qs + 16);
+      br.q[0] = a.x; br.q[1] = a.y; br.q[2] = a.z; br.q[3] = a.w;
+      br.q[4] = b.x; br.q[5] = b.y; br.q[6] = b.z; br.q[7] = b.w;
+    } else if constexpr (R::BPT == 16) {
+      const uint4 a = *reinterpret_cast<const uint4*>(qs);
+      br.q[0] = a.x; br.q[1] = a.y; br.q[2] = a.z; br.q[3] = a.w;
+    } else {
+      const uint2 a = *reinterpret_cast<const uint2*>(qs);
+      br.q[0] = a.x; br.q[1] = a.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R::F16_LOADS; i++) {
+      const int idx = i * NT + tid, r = idx >> 3, c8 = (idx & 7) * 8;
+      const void* W;
+      int n;
+      brow<EPI>(r, n0, p, W, n);
+      br.f[i] = *reinterpret_cast<const uint4*>((const _Float16*)W + (size_t)n * p.K + kt * BK + c8);
+    }
+  }
+}
+
+template <int WF, int NT>
+__device__ __forceinline__ void store_b(const BRaw<WF, NT>& br, _Float16* Bs, int kt, int tid) {
+  using R = BRaw<WF, NT>;
+  if (WF == WF_Q4K) {
+    const int r = tid / R::TPR, part = tid % R::TPR;
+    const int c = ((kt * BK) % QK_K) / 64;
+    float s0, o0, s1, o1;
+    chunk_scales(br.hd, c, s0, o0, s1, o1);
+    _Float16* row = Bs + r * LDSK;
+#pragma unroll
+    for (int w = 0; w < R::BPT / 4; w++) {
+      h4 lo, hi;
+      deq4(br.q[w], s0, o0, s1, o1, lo, hi);
+      *reinterpret_cast<h4*>(row + part * R::BPT + 4 * w) = lo;
+      *reinterpret_cast<h4*>(row + 32 + part * R::BPT + 4 * w) = hi;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R::F16_LOADS; i++) {
+      const int idx = i * NT + tid, r = idx >> 3, c8 = (idx & 7) * 8;
+      *reinterpret_cast<uint4*>(Bs + r * LDSK + c8) = br.f[i];
+    }
+  }
+}
+
+template <int EPI, int WF, int MW>
+__global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+  constexpr int NT = 64 * MW, BM = 64 * MW;
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
 
+  // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous tile range.
+  const int per_xcd = gridDim.x / 8;
+  const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= tiles_m * tiles_n) return;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * (EPI == EPI_GATED ? BN / 2 : BN);
-  const int K = p.K;
-  const int nkt = K / BK;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = tm * BM;
+  const int n0 = tn * (EPI == EPI_GATED ? BN / 2 : BN);
+  const int nkt = p.K / BK;
 
-  // ---- A tile loader: 4 x 16 B per thread ----
-  const _Float16* Ag = p.A + (size_t)m0 * p.lda;
-  uint4 areg[4];
-  auto load_a = [&](int kt) {
+  const _Float16* arow[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = i * 32 + (tid >> 3), c = (tid & 7) * 8;
-      areg[i] = *reinterpret_cast<const uint4*>(Ag + (size_t)r * p.lda + kt * BK + c);
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = i * 32 + (tid >> 3), c = (tid & 7) * 8;
-      *reinterpret_cast<uint4*>(&As[buf][r * LDSK + c]) = areg[i];
-    }
-  };
+  for (int mb = 0; mb < 4; mb++) arow[mb] = p.A + (size_t)(m0 + wave * 64 + mb * 16 + lr) * p.lda + 16 * lg;
 
-  // ---- B tile loader ----
-  // Q4_K: thread -> (row r = tid/2, half h = tid%2): header 16 B + 16 B of nibbles.
-  // f16:  same pattern as A (4 x 16 B per thread).
-  uint4 breg[4];
-  const int kblocks = K / QK_K;
-  auto load_b = [&](int kt) {
-    if (WF == WF_Q4K) {
-      const int r = tid >> 1, h = tid & 1;
-      int mat, n;
-      brow_map<EPI>(r, n0, mat, n);
-      const uint8_t* W = (const uint8_t*)(mat ? p.W1 : p.W0);
-      const int kb = (kt * BK) / QK_K, chunk = ((kt * BK) % QK_K) / 64;
-      const uint8_t* blk = W + ((size_t)n * kblocks + kb) * Q4K_BYTES;
-      breg[0] = *reinterpret_cast<const uint4*>(blk);
-      breg[1] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * chunk + 16 * h);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = i * 32 + (tid >> 3), c = (tid & 7) * 8;
-        int mat, n;
-        brow_map<EPI>(r, n0, mat, n);
-        const _Float16* W = (const _Float16*)(mat ? p.W1 : p.W0);
-        breg[i] = *reinterpret_cast<const uint4*>(W + (size_t)n * K + kt * BK + c);
-      }
-    }
-  };
-  auto store_b = [&](int buf, int kt) {
-    if (WF == WF_Q4K) {
-      const int r = tid >> 1, h = tid & 1;
-      const int chunk = ((kt * BK) % QK_K) / 64;
-      const uint4 hd = breg[0];
-      const float d = f16_bits_to_f32(hd.x & 0xffff), dmin = f16_bits_to_f32(hd.x >> 16);
-      int sc0, mn0, sc1, mn1;
-      scale_min_u32(hd.y, hd.z, hd.w, 2 * chunk, sc0, mn0);
-      scale_min_u32(hd.y, hd.z, hd.w, 2 * chunk + 1, sc1, mn1);
-      const float s0 = d * (float)sc0, o0 = dmin * (float)mn0;
-      const float s1 = d * (float)sc1, o1 = dmin * (float)mn1;
-      const uint32_t q[4] = {breg[1].x, breg[1].y, breg[1].z, breg[1].w};
-      h8 lo[2], hi[2];
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-#pragma unroll
-        for (int bb = 0; bb < 4; bb++) {
-          const uint32_t byte = (q[w] >> (8 * bb)) & 0xff;
-          const int e = w * 4 + bb;  // 0..15
-          lo[e >> 3][e & 7] = (_Float16)(s0 * (float)(byte & 15) - o0);
-          hi[e >> 3][e & 7] = (_Float16)(s1 * (float)(byte >> 4) - o1);
-        }
-      }
-      _Float16* row = &Bs[buf][r * LDSK];
-      *reinterpret_cast<h8*>(row + 16 * h) = lo[0];
-      *reinterpret_cast<h8*>(row + 16 * h + 8) = lo[1];
-      *reinterpret_cast<h8*>(row + 32 + 16 * h) = hi[0];
-      *reinterpret_cast<h8*>(row + 32 + 16 * h + 8) = hi[1];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = i * 32 + (tid >> 3), c = (tid & 7) * 8;
-        *reinterpret_cast<uint4*>(&Bs[buf][r * LDSK + c]) = breg[i];
-      }
-    }
-  };
-
-  f4 acc[4][4];
+  f4 acc[4][8];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 8; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  store_b(0, 0);
-  __syncthreads();
+  uint4 a0[4][2], a1[4][2];
+  BRaw<WF, NT> br;
 
-  const int lr = lane & 15, lk = (lane >> 4) * 8;
-  for (int kt = 0; kt < nkt; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      h8 a[4], b[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-        a[mi] = *reinterpret_cast<const h8*>(&As[buf][(wm * 64 + mi * 16 + lr) * LDSK + ks * 32 + lk]);
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++)
-        b[ni] = *reinterpret_cast<const h8*>(&Bs[buf][(wn * 64 + ni * 16 + lr) * LDSK + ks * 32 + lk]);
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 4; ni++)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-    }
-    if (kt + 1 < nkt) {
-      store_a(buf ^ 1);
-      store_b(buf ^ 1, kt + 1);
-    }
-    __syncthreads();
+#define LOAD_A(dst, kt)                                                                     \
+  _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                        \
+    dst[mb][0] = *reinterpret_cast<const uint4*>(arow[mb] + (kt) * BK);                     \
+    dst[mb][1] = *reinterpret_cast<const uint4*>(arow[mb] + (kt) * BK + 8);                 \
+  }
+#define COMPUTE(areg, buf)                                                                  \
+  _Pragma("unroll") for (int s = 0; s < 2; s++) {                                           \
+    h8 bf[8];                                                                               \
+    _Pragma("unroll") for (int nb = 0; nb < 8; nb++) bf[nb] =                               \
+        *reinterpret_cast<const h8*>(&Bs[buf][(nb * 16 + lr) * LDSK + 16 * lg + 8 * s]);    \
+    _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                      \
+      const h8 af = __builtin_bit_cast(h8, areg[mb][s]);                                    \
+      _Pragma("unroll") for (int nb = 0; nb < 8; nb++) acc[mb][nb] =                        \
+          __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);         \
+    }                                                                                       \
   }
 
-  // ---- epilogue: lane holds D[row 4*(lane/16)+i][col lane%16] of each 16x16 block ----
-  const int rbase = m0 + wm * 64 + (lane >> 4) * 4;
+  load_b<EPI, WF, NT>(br, p, n0, 0, tid);
+  LOAD_A(a0, 0);
+  store_b<WF, NT>(br, Bs[0], 0, tid);
+  __syncthreads();
+  // Drain every counter once here: otherwise the prologue's A loads are still pending at
+  // the loop header, and the wait that covers them lands inside the loop body, where in
+  // steady state it would stall each step on the *next* step's prefetch.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // One MFMA site per iteration keeps the accumulators in place (no AGPR<->VGPR copies);
+  // the next step's A and B are in flight while this step's MFMAs run.
+  for (int kt = 0; kt < nkt; kt++) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < nkt;
+    if (more) {  // B first: store_b below then waits only for the B loads
+      load_b<EPI, WF, NT>(br, p, n0, kt + 1, tid);
+      LOAD_A(a1, kt + 1);
+    }
+    COMPUTE(a0, buf);
+    if (more) store_b<WF, NT>(br, Bs[buf ^ 1], kt + 1, tid);
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+      a0[mb][0] = a1[mb][0];
+      a0[mb][1] = a1[mb][1];
+    }
+  }
+#undef LOAD_A
+#undef COMPUTE
+
+  // ---- epilogue: lane holds D[row 4*lg+i][col lr] of each 16x16 block ----
+  const int rbase = m0 + wave * 64 + lg * 4;
   if (EPI == EPI_GATED) {
     _Float16* out = (_Float16*)p.out;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-      for (int ni = 0; ni < 2; ni++) {
-        const int n = n0 + wn * 32 + ni * 16 + lr;
+      for (int nb = 0; nb < 4; nb++) {
+        const int n = n0 + nb * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int m = rbase + mi * 16 + i;
-          if (m < p.M) {
-            const float g = acc[mi][ni][i], u = acc[mi][ni + 2][i];
-            out[(size_t)m * p.ldo + n] = (_Float16)(gelu_tanh_dev(g) * u);
-          }
+          const int m = rbase + mb * 16 + i;
+          if (m < p.M) out[(size_t)m * p.ldo + n] = (_Float16)(gelu_tanh_dev(acc[mb][nb][i]) * acc[mb][nb + 4][i]);
         }
       }
   } else {
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-      for (int ni = 0; ni < 4; ni++) {
-        const int n = n0 + wn * 64 + ni * 16 + lr;
+      for (int nb = 0; nb < 8; nb++) {
+        const int n = n0 + nb * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int m = rbase + mi * 16 + i;
+          const int m = rbase + mb * 16 + i;
           if (m >= p.M) continue;
-          const float v = acc[mi][ni][i];
+          const float v = acc[mb][nb][i];
           if (EPI == EPI_F16) {
             ((_Float16*)p.out)[(size_t)m * p.ldo + n] = (_Float16)v;
           } else if (EPI == EPI_RELU) {
@@ -235,31 +268,57 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p) {
   }
 }
 
-template <int EPI>
-hipError_t launch_epi(int wfmt, const GemmArgs& a, hipStream_t s) {
+template <int EPI, int WF>
+hipError_t launch_mw(int mw, const GemmArgs& a, hipStream_t s) {
   const int bn = EPI == EPI_GATED ? BN / 2 : BN;
-  dim3 grid(a.N / bn, (a.M + BM - 1) / BM);
-  if (wfmt == WF_Q4K)
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF_Q4K>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF_F16>), grid, dim3(256), 0, s, a);
+  const int tiles_n = a.N / bn, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
+  const int tiles = tiles_m * tiles_n;
+  const int grid = (tiles + 7) / 8 * 8;
+  switch (mw) {
+    case 2: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2>), dim3(grid), dim3(128), 0, s, a, tiles_m, tiles_n); break;
+    case 4: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n); break;
+    default: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 8>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n); break;
+  }
   return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_epi(int wfmt, int mw, const GemmArgs& a, hipStream_t s) {
+  return wfmt == WF_Q4K ? launch_mw<EPI, WF_Q4K>(mw, a, s) : launch_mw<EPI, WF_F16>(mw, a, s);
 }
 
 }  // namespace
 
 namespace t5k {
-// Shapes are validated by the caller: N % 128 == 0 (N % 64 for gated), K % 256 == 0,
-// A allocated with at least roundup(M, 128) rows.
-hipError_t launch_gemm(int epi, int wfmt, const GemmArgs& a, hipStream_t s) {
+// Rows per workgroup tile: 64 * mw, mw in {2, 4, 8}.  The caller guarantees N % 128 == 0
+// (N % 64 for gated), K % 256 == 0, and A rows allocated up to roundup(M, 512).
+// n_tiles = number of 128-row weight tiles.  Picks the tile height that needs the fewest
+// rounds of workgroups over the device (a round of 8-wave tiles costs about twice a round
+// of 4-wave tiles); ties go to the taller tile, which re-dequantizes less per token.
+int gemm_pick_mw(int M, int n_tiles, int cus) {
+  int best = 8;
+  double best_cost = 1e30;
+  for (int mw : {8, 4, 2}) {
+    const long tiles = (long)((M + 64 * mw - 1) / (64 * mw)) * n_tiles;
+    const long rounds = (tiles + cus - 1) / cus;
+    const double cost = rounds * (double)mw;
+    if (cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best = mw;
+    }
+  }
+  return best;
+}
+
+hipError_t launch_gemm(int epi, int wfmt, int mw, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   switch (epi) {
-    case EPI_F16: return launch_epi<EPI_F16>(wfmt, a, s);
-    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, a, s);
-    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, a, s);
-    case EPI_F32: return launch_epi<EPI_F32>(wfmt, a, s);
-    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, a, s);
-    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, a, s);
+    case EPI_F16: return launch_epi<EPI_F16>(wfmt, mw, a, s);
+    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, mw, a, s);
+    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, mw, a, s);
+    case EPI_F32: return launch_epi<EPI_F32>(wfmt, mw, a, s);
+    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, mw, a, s);
+    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, mw, a, s);
   }
   return hipErrorInvalidValue;
 }

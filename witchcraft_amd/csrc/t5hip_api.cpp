@@ -11,7 +11,7 @@
 
 #include <algorithm>
 #include <memory>
-#include <mutex>
+#include <stdlib.h>
 #include <string>
 #include <vector>
 
@@ -80,6 +80,9 @@ struct t5h_model {
   int device = 0;
   hipStream_t stream = nullptr;
   int inner = 0;
+  int cus = 256;          // compute units of the device
+  int gemm_mw_override = 0;  // T5H_GEMM_MW / T5H_GEMM_BN tuning knobs (0 = heuristic)
+  int gemm_bn_override = 0;
 
   // ---- weights (one device arena) ----
   void* arena = nullptr;
@@ -240,7 +243,8 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   if (T <= m->cap_tokens && B <= m->cap_seqs && nwork <= m->cap_work) return T5H_OK;
   const int capT = std::max(T, m->cap_tokens), capB = std::max(B, m->cap_seqs);
   const int capW = std::max(nwork, m->cap_work);
-  const int tpad = (capT + 127) / 128 * 128 + 128;
+  // GEMM tiles read A rows up to roundup(T, 512); attention reads up to T + 63.
+  const int tpad = (capT + 511) / 512 * 512 + 128;
   const t5h_config& c = m->cfg;
   size_t off = 0;
   auto take = [&](size_t n) {
@@ -374,7 +378,10 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
                            (epi == EPI_RESID ? 2.0 : 1.0);
   const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
   Timed t(m, kind, flops, bytes);
-  HIP_OK(t5k::launch_gemm(epi, W.fmt, a, m->stream));
+  const int n_tiles = W.N * (W1 ? 2 : 1) / 128;
+  int mw = t5k::gemm_pick_mw(M, n_tiles, m->cus);
+  if (m->gemm_mw_override) mw = m->gemm_mw_override;
+  HIP_OK(t5k::launch_gemm(epi, W.fmt, mw, a, m->stream));
   return T5H_OK;
 }
 
@@ -585,6 +592,15 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   m->cfg = *cfg;
   m->device = dev;
   m->inner = cfg->num_heads * cfg->d_kv;
+  m->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  if (const char* e = getenv("T5H_GEMM_MW")) {
+    const int v = atoi(e);
+    if (v == 2 || v == 4 || v == 8) m->gemm_mw_override = v;
+  }
+  if (const char* e = getenv("T5H_GEMM_BN")) {
+    const int v = atoi(e);
+    if (v == 64 || v == 128) m->gemm_bn_override = v;
+  }
   const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
 
   HostArena ha;
