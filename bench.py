@@ -89,7 +89,20 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB 10 times (the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 10}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU (got --gpus {args.gpus}); sequences are "
               "independent, so N GPUs would each run this workload on their own share.", file=sys.stderr)
@@ -155,14 +168,23 @@ def main() -> None:
             k["gbs"] = s["bytes"] / (s["total_ms"] * 1e-3) / 1e9
             k["hbm_frac"] = k["gbs"] / PEAK_HBM_GBS
         kernels[name] = k
-    dom = stats["gemm_ffn_gate_up"]
+    # dominant kernel = the GEMM class with the largest share of the step
+    gemms = {k: v for k, v in stats.items() if k.startswith("gemm_") and v["launches"]}
+    dom_name = max(gemms, key=lambda k: gemms[k]["total_ms"])
+    dom = gemms[dom_name]
     avg_s = dom["total_ms"] / dom["launches"] * 1e-3
     flops_per_launch = dom["flops"] / dom["launches"]
     achieved = flops_per_launch / avg_s / 1e12
-    roofline = {"kernel": "gemm_ffn_gate_up (wi_0|wi_1 Q4_K dequant-GEMM + gelu*up epilogue)",
+    traffic = None
+    tfile = ROOT / "profiles" / "encoder_cfg2_traffic.json"
+    if args.workload == "cfg2" and args.seed == 0 and tfile.exists():
+        t = json.loads(tfile.read_text())["bytes_per_dispatch"].get(dom_name)
+        traffic = t["fetch"] + t["write"] if t else None
+    roofline = {"kernel": f"{dom_name} (Q4_K dequant-GEMM, v_mfma_f32_16x16x32_f16)",
                 "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
-                "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6}
+                "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
+                "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6,
+                "share_of_step": dom["total_ms"] / sum(v["total_ms"] for v in stats.values())}
 
     base = None
     if not args.no_cpu_baseline:

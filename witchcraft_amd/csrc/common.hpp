@@ -68,8 +68,8 @@ __device__ __forceinline__ float gelu_tanh_dev(float x) {
 // Host-side launchers (defined in the .hip files) --------------------------------
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
-hipError_t launch_gemm(int epi, int wfmt, int mw, const GemmArgs& a, hipStream_t s);
-int gemm_pick_mw(int M, int n_tiles, int cus);
+hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s);
+void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
                         float* x, unsigned* err_flag, hipStream_t s);

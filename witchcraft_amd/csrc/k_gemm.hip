@@ -4,7 +4,7 @@
 // super-blocks (or f16).  Reference: every linear of the encoder, candle QMatMul /
 // f32 matmul (src/quantized_t5.rs:383-424 QKV, :501 O, :231-252 FFN, :700 projection).
 //
-// Workgroup = MW wave64s stacked along M; tile BM = 64*MW tokens x BN = 128 weight rows,
+// Workgroup = MW wave64s stacked along M; tile BM = 64*MW tokens x BN = 128 or 64 weight rows,
 // K stepped by 64 (one Q4_K chunk: sub-blocks 2c and 2c+1 of every row).
 //  * B (weights): each K step the workgroup reads, per weight row, the 16-byte Q4_K header
 //    (d, dmin, 12 scale bytes) and 32 bytes of packed nibbles, dequantizes them with f32
@@ -16,14 +16,14 @@
 //    (K = 16g .. 16g+15) of its row, so the 4 lane groups cover one 128-byte line per row.
 //    MFMA step s (of 2) uses K = 16g + 8s + 0..7; the B fragments are read from LDS with
 //    the same K order, so the product is the plain dot product.
-//  * Each wave holds 64 x 128 f32 accumulators (4 x 8 blocks of 16x16).
+//  * Each wave holds 64 x BN f32 accumulators (4 x BN/16 blocks of 16x16).
 //  * Tiles are ordered so that each XCD (8 per device, workgroups dealt round-robin) works
 //    on a contiguous band of M tiles: its L2 holds the A rows it streams plus the weights.
 #include "common.hpp"
 
 namespace {
 
-constexpr int BN = 128, BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 reads
+constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 reads
 
 __device__ __forceinline__ int sbyte(const uint4& hd, int i) {
   // byte i (0..11) of the 12 packed scale bytes = header bytes 4..15
@@ -63,11 +63,11 @@ __device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, f
           (_Float16)(s1 * (float)((h >> 16) & 0xff) - o1), (_Float16)(s1 * (float)(h >> 24) - o1)};
 }
 
-template <int EPI>
+template <int EPI, int BN>
 __device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const void*& W, int& n) {
-  if (EPI == EPI_GATED) {  // rows [0,64): W0 columns n0.., rows [64,128): W1 same columns
-    W = r < 64 ? p.W0 : p.W1;
-    n = n0 + (r & 63);
+  if (EPI == EPI_GATED) {  // rows [0,BN/2): W0 columns n0.., rows [BN/2,BN): W1 same columns
+    W = r < BN / 2 ? p.W0 : p.W1;
+    n = n0 + (r & (BN / 2 - 1));
   } else {
     W = p.W0;
     n = n0 + r;
@@ -75,7 +75,7 @@ __device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const voi
 }
 
 // Raw B data of one K step held in registers between the global load and the LDS store.
-template <int WF, int NT>
+template <int WF, int NT, int BN>
 struct BRaw {
   static constexpr int TPR = NT / BN;           // threads per weight row (Q4_K)
   static constexpr int BPT = 32 / TPR;          // nibble bytes per thread
@@ -85,14 +85,14 @@ struct BRaw {
   uint4 f[WF == WF_F16 ? F16_LOADS : 1];
 };
 
-template <int EPI, int WF, int NT>
-__device__ __forceinline__ void load_b(BRaw<WF, NT>& br, const GemmArgs& p, int n0, int kt, int tid) {
-  using R = BRaw<WF, NT>;
+template <int EPI, int WF, int NT, int BN>
+__device__ __forceinline__ void load_b(BRaw<WF, NT, BN>& br, const GemmArgs& p, int n0, int kt, int tid) {
+  using R = BRaw<WF, NT, BN>;
   if (WF == WF_Q4K) {
     const int r = tid / R::TPR, part = tid % R::TPR;
     const void* W;
     int n;
-    brow<EPI>(r, n0, p, W, n);
+    brow<EPI, BN>(r, n0, p, W, n);
     const int kb = (kt * BK) / QK_K, c = ((kt * BK) % QK_K) / 64;
     const uint8_t* blk = (const uint8_t*)W + ((size_t)n * (p.K / QK_K) + kb) * Q4K_BYTES;
     br.hd = *reinterpret_cast<const uint4*>(blk);
@@ -114,15 +114,15 @@ __device__ __forceinline__ void load_b(BRaw<WF, NT>& br, const GemmArgs& p, int 
       const int idx = i * NT + tid, r = idx >> 3, c8 = (idx & 7) * 8;
       const void* W;
       int n;
-      brow<EPI>(r, n0, p, W, n);
+      brow<EPI, BN>(r, n0, p, W, n);
       br.f[i] = *reinterpret_cast<const uint4*>((const _Float16*)W + (size_t)n * p.K + kt * BK + c8);
     }
   }
 }
 
-template <int WF, int NT>
-__device__ __forceinline__ void store_b(const BRaw<WF, NT>& br, _Float16* Bs, int kt, int tid) {
-  using R = BRaw<WF, NT>;
+template <int WF, int NT, int BN>
+__device__ __forceinline__ void store_b(const BRaw<WF, NT, BN>& br, _Float16* Bs, int kt, int tid) {
+  using R = BRaw<WF, NT, BN>;
   if (WF == WF_Q4K) {
     const int r = tid / R::TPR, part = tid % R::TPR;
     const int c = ((kt * BK) % QK_K) / 64;
@@ -145,9 +145,9 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NT>& br, _Float16* Bs, in
   }
 }
 
-template <int EPI, int WF, int MW>
+template <int EPI, int WF, int MW, int BN>
 __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
-  constexpr int NT = 64 * MW, BM = 64 * MW;
+  constexpr int NT = 64 * MW, BM = 64 * MW, NB = BN / 16;
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
 
   // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous tile range.
@@ -166,14 +166,14 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
   for (int mb = 0; mb < 4; mb++) arow[mb] = p.A + (size_t)(m0 + wave * 64 + mb * 16 + lr) * p.lda + 16 * lg;
 
-  f4 acc[4][8];
+  f4 acc[4][NB];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   uint4 a0[4][2], a1[4][2];
-  BRaw<WF, NT> br;
+  BRaw<WF, NT, BN> br;
 
 #define LOAD_A(dst, kt)                                                                     \
   _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                        \
@@ -182,19 +182,19 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 #define COMPUTE(areg, buf)                                                                  \
   _Pragma("unroll") for (int s = 0; s < 2; s++) {                                           \
-    h8 bf[8];                                                                               \
-    _Pragma("unroll") for (int nb = 0; nb < 8; nb++) bf[nb] =                               \
+    h8 bf[NB];                                                                              \
+    _Pragma("unroll") for (int nb = 0; nb < NB; nb++) bf[nb] =                              \
         *reinterpret_cast<const h8*>(&Bs[buf][(nb * 16 + lr) * LDSK + 16 * lg + 8 * s]);    \
     _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                      \
       const h8 af = __builtin_bit_cast(h8, areg[mb][s]);                                    \
-      _Pragma("unroll") for (int nb = 0; nb < 8; nb++) acc[mb][nb] =                        \
+      _Pragma("unroll") for (int nb = 0; nb < NB; nb++) acc[mb][nb] =                       \
           __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);         \
     }                                                                                       \
   }
 
-  load_b<EPI, WF, NT>(br, p, n0, 0, tid);
+  load_b<EPI, WF, NT, BN>(br, p, n0, 0, tid);
   LOAD_A(a0, 0);
-  store_b<WF, NT>(br, Bs[0], 0, tid);
+  store_b<WF, NT, BN>(br, Bs[0], 0, tid);
   __syncthreads();
   // Drain every counter once here: otherwise the prologue's A loads are still pending at
   // the loop header, and the wait that covers them lands inside the loop body, where in
@@ -207,11 +207,11 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int buf = kt & 1;
     const bool more = kt + 1 < nkt;
     if (more) {  // B first: store_b below then waits only for the B loads
-      load_b<EPI, WF, NT>(br, p, n0, kt + 1, tid);
+      load_b<EPI, WF, NT, BN>(br, p, n0, kt + 1, tid);
       LOAD_A(a1, kt + 1);
     }
     COMPUTE(a0, buf);
-    if (more) store_b<WF, NT>(br, Bs[buf ^ 1], kt + 1, tid);
+    if (more) store_b<WF, NT, BN>(br, Bs[buf ^ 1], kt + 1, tid);
     __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) {
@@ -229,19 +229,19 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-      for (int nb = 0; nb < 4; nb++) {
+      for (int nb = 0; nb < NB / 2; nb++) {
         const int n = n0 + nb * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int m = rbase + mb * 16 + i;
-          if (m < p.M) out[(size_t)m * p.ldo + n] = (_Float16)(gelu_tanh_dev(acc[mb][nb][i]) * acc[mb][nb + 4][i]);
+          if (m < p.M) out[(size_t)m * p.ldo + n] = (_Float16)(gelu_tanh_dev(acc[mb][nb][i]) * acc[mb][nb + NB / 2][i]);
         }
       }
   } else {
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-      for (int nb = 0; nb < 8; nb++) {
+      for (int nb = 0; nb < NB; nb++) {
         const int n = n0 + nb * 16 + lr;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -268,57 +268,58 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
-template <int EPI, int WF>
-hipError_t launch_mw(int mw, const GemmArgs& a, hipStream_t s) {
-  const int bn = EPI == EPI_GATED ? BN / 2 : BN;
-  const int tiles_n = a.N / bn, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
-  const int tiles = tiles_m * tiles_n;
-  const int grid = (tiles + 7) / 8 * 8;
+template <int EPI, int WF, int BN>
+hipError_t launch_cfg(int mw, const GemmArgs& a, hipStream_t s) {
+  const int cols = EPI == EPI_GATED ? BN / 2 : BN;
+  const int tiles_n = a.N / cols, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
+  const int grid = (tiles_m * tiles_n + 7) / 8 * 8;
   switch (mw) {
-    case 2: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2>), dim3(grid), dim3(128), 0, s, a, tiles_m, tiles_n); break;
-    case 4: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n); break;
-    default: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 8>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN>), dim3(grid), dim3(128), 0, s, a, tiles_m, tiles_n); break;
+    case 4: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n); break;
+    default: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 8, BN>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n); break;
   }
   return hipGetLastError();
 }
 
 template <int EPI>
-hipError_t launch_epi(int wfmt, int mw, const GemmArgs& a, hipStream_t s) {
-  return wfmt == WF_Q4K ? launch_mw<EPI, WF_Q4K>(mw, a, s) : launch_mw<EPI, WF_F16>(mw, a, s);
+hipError_t launch_epi(int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s) {
+  if (wfmt == WF_Q4K)
+    return bn == 64 ? launch_cfg<EPI, WF_Q4K, 64>(mw, a, s) : launch_cfg<EPI, WF_Q4K, 128>(mw, a, s);
+  return bn == 64 ? launch_cfg<EPI, WF_F16, 64>(mw, a, s) : launch_cfg<EPI, WF_F16, 128>(mw, a, s);
 }
 
 }  // namespace
 
 namespace t5k {
-// Rows per workgroup tile: 64 * mw, mw in {2, 4, 8}.  The caller guarantees N % 128 == 0
-// (N % 64 for gated), K % 256 == 0, and A rows allocated up to roundup(M, 512).
-// n_tiles = number of 128-row weight tiles.  Picks the tile height that needs the fewest
-// rounds of workgroups over the device (a round of 8-wave tiles costs about twice a round
-// of 4-wave tiles); ties go to the taller tile, which re-dequantizes less per token.
-int gemm_pick_mw(int M, int n_tiles, int cus) {
-  int best = 8;
-  double best_cost = 1e30;
-  for (int mw : {8, 4, 2}) {
-    const long tiles = (long)((M + 64 * mw - 1) / (64 * mw)) * n_tiles;
-    const long rounds = (tiles + cus - 1) / cus;
-    const double cost = rounds * (double)mw;
-    if (cost < best_cost - 1e-9) {
-      best_cost = cost;
-      best = mw;
-    }
+// Tile choice for C[M, N]: rows 64*mw (mw in {2, 4, 8}) x bn weight rows (64 or 128).
+// Measured on MI355X for every encoder GEMM (N = 128..4096, K = 768/2048, M = 32..73728):
+// the 4-wave x 128-row tile is fastest once it yields >= 1.4 tiles per CU; below that the
+// 4-wave x 64-row tile while it still covers >= 0.75 of the CUs; otherwise 2-wave x 64-row
+// tiles (small token counts, where latency dominates).  n_rows = weight rows of the launch
+// (both matrices for the gated FFN).
+void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn) {
+  auto tiles = [&](int w, int b) { return (double)((M + 64 * w - 1) / (64 * w)) * (n_rows / b); };
+  if (n_rows % 128 == 0 && tiles(4, 128) >= 1.4 * cus) {
+    mw = 4;
+    bn = 128;
+  } else if (tiles(4, 64) >= 0.75 * cus) {
+    mw = 4;
+    bn = 64;
+  } else {
+    mw = 2;
+    bn = 64;
   }
-  return best;
 }
 
-hipError_t launch_gemm(int epi, int wfmt, int mw, const GemmArgs& a, hipStream_t s) {
+hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   switch (epi) {
-    case EPI_F16: return launch_epi<EPI_F16>(wfmt, mw, a, s);
-    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, mw, a, s);
-    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, mw, a, s);
-    case EPI_F32: return launch_epi<EPI_F32>(wfmt, mw, a, s);
-    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, mw, a, s);
-    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, mw, a, s);
+    case EPI_F16: return launch_epi<EPI_F16>(wfmt, mw, bn, a, s);
+    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, mw, bn, a, s);
+    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, mw, bn, a, s);
+    case EPI_F32: return launch_epi<EPI_F32>(wfmt, mw, bn, a, s);
+    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, mw, bn, a, s);
+    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, mw, bn, a, s);
   }
   return hipErrorInvalidValue;
 }

@@ -378,10 +378,11 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
                            (epi == EPI_RESID ? 2.0 : 1.0);
   const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
   Timed t(m, kind, flops, bytes);
-  const int n_tiles = W.N * (W1 ? 2 : 1) / 128;
-  int mw = t5k::gemm_pick_mw(M, n_tiles, m->cus);
+  int mw, bn;
+  t5k::gemm_pick_tile(M, W.N * (W1 ? 2 : 1), m->cus, mw, bn);
   if (m->gemm_mw_override) mw = m->gemm_mw_override;
-  HIP_OK(t5k::launch_gemm(epi, W.fmt, mw, a, m->stream));
+  if (m->gemm_bn_override) bn = m->gemm_bn_override;
+  HIP_OK(t5k::launch_gemm(epi, W.fmt, mw, bn, a, m->stream));
   return T5H_OK;
 }
 
