@@ -19,17 +19,27 @@ enum EmbFmt : int { EMB_F32 = 0, EMB_Q4K = 1 };
 
 // GEMM epilogues.
 enum Epilogue : int {
-  EPI_F16 = 0,    // out f16 [M][ldo]
+  EPI_F16 = 0,    // out f16 [M][ldo] in operand order (tiled_index)
   EPI_RESID = 1,  // resid f32 [M][ldo] += acc
-  EPI_GATED = 2,  // out f16 = gelu_tanh(acc(W0)) * acc(W1)
+  EPI_GATED = 2,  // out f16 = gelu_tanh(acc(W0)) * acc(W1), operand order
   EPI_F32 = 3,    // out f32 [M][ldo]
   EPI_QKV = 4,    // q/k/v f16 head-major [3][H][tpad][dkv]
-  EPI_RELU = 5    // out f16 = max(acc, 0) (non-gated T5DenseActDense)
+  EPI_RELU = 5    // out f16 = max(acc, 0), operand order (non-gated T5DenseActDense)
 };
 
+// Activations that feed a GEMM (RMSNorm output, attention output, gated hidden state) are
+// stored in "MFMA operand order": the [M][K] f16 matrix is cut into 16-row x 32-column
+// blocks of 1 KiB, blocks row-major ([M/16][K/32]), and inside a block lane l of a wave64
+// owns the 16 bytes at l*16 = row (l % 16), columns 8*(l / 16) .. +7 -- exactly the
+// register layout of a v_mfma_f32_16x16x32_f16 operand.  A wave loads one operand with one
+// fully contiguous 1 KiB dwordx4 load.  M must be padded to a multiple of 16, K % 32 == 0.
+__host__ __device__ __forceinline__ size_t tiled_index(size_t m, size_t k, size_t K) {
+  return ((m >> 4) * (K >> 5) + (k >> 5)) * 512 + ((((k & 31) >> 3) << 4) + (m & 15)) * 8 + (k & 7);
+}
+
 struct GemmArgs {
-  const _Float16* A;  // [Mpad][lda] f16, Mpad >= roundup(M, 128)
-  int lda;
+  const _Float16* A;  // [Mpad][K] f16 in operand order (tiled_index), Mpad >= roundup(M, 512)
+  int lda;            // unused (A's row length is K)
   const void* W0;  // [N][K] weights (Q4_K blocks row-major along K, or f16)
   const void* W1;  // second weight for EPI_GATED
   int M, N, K;     // N counts output columns (per weight for EPI_GATED)
@@ -41,7 +51,7 @@ struct GemmArgs {
 
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]
-  _Float16* out;        // [T][H*dkv]
+  _Float16* out;        // [T][H*dkv] in operand order (tiled_index)
   const int* cu;        // [B+1] device
   const int2* work;     // (seq, q_tile) pairs
   const float* lut;     // [H][2*maxl-1] relative bias by (j - i)
@@ -57,12 +67,13 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   return (float)h;
 }
 
-// candle Tensor::gelu (tanh form) with tanh(u) = 1 - 2/(exp(2u)+1).
+// candle Tensor::gelu (tanh form): 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
+// evaluated as the identical x * sigmoid(2u) = x / (1 + 2^(-2u log2 e)).
 __device__ __forceinline__ float gelu_tanh_dev(float x) {
-  const float u = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
-  const float e = __expf(2.0f * u);
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  return 0.5f * x * (1.0f + t);
+  const float x2 = x * x;
+  const float u = x * (0.7978845608028654f + 0.0356774081363001f * x2);
+  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Host-side launchers (defined in the .hip files) --------------------------------
@@ -76,7 +87,7 @@ hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, 
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
                           hipStream_t s);
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s);
-hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, hipStream_t s);
+hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s);
 hipError_t launch_window_sum(const float* win_out, const int* src_rows, int n_tokens, int max_windows,
                              int P, float* sum, float* norm, float* normalized, hipStream_t s);
 }  // namespace t5k

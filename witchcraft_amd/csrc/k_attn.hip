@@ -135,14 +135,14 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
     __syncthreads();
   }
 
-  if (qi < L) {
+  if (qi < L) {  // written in operand order for the O GEMM
     const float inv = 1.0f / l_run;
-    _Float16* orow = p.out + (size_t)(s0 + qi) * (p.heads * DK) + h * DK;
+    const int inner = p.heads * DK;
 #pragma unroll
     for (int db = 0; db < 4; db++) {
       const h4 v = {(_Float16)(o[db][0] * inv), (_Float16)(o[db][1] * inv), (_Float16)(o[db][2] * inv),
                     (_Float16)(o[db][3] * inv)};
-      *reinterpret_cast<h4*>(orow + db * 16 + lg * 4) = v;
+      *reinterpret_cast<h4*>(p.out + tiled_index(s0 + qi, h * DK + db * 16 + lg * 4, inner)) = v;
     }
   }
 }

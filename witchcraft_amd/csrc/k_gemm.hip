@@ -4,26 +4,31 @@
 // super-blocks (or f16).  Reference: every linear of the encoder, candle QMatMul /
 // f32 matmul (src/quantized_t5.rs:383-424 QKV, :501 O, :231-252 FFN, :700 projection).
 //
-// Workgroup = MW wave64s stacked along M; tile BM = 64*MW tokens x BN = 128 or 64 weight rows,
-// K stepped by 64 (one Q4_K chunk: sub-blocks 2c and 2c+1 of every row).
-//  * B (weights): each K step the workgroup reads, per weight row, the 16-byte Q4_K header
-//    (d, dmin, 12 scale bytes) and 32 bytes of packed nibbles, dequantizes them with f32
-//    scale/min math (one rounding to f16 per value) and stores the 128x64 f16 tile in LDS,
-//    double-buffered.  Every wave consumes the whole tile, so the dequantization is
-//    amortised over BM tokens.
-//  * A (activations): each wave owns 64 rows and streams them straight from global memory
-//    into VGPRs -- no LDS round trip.  A lane of lane-group g reads 32 contiguous bytes
-//    (K = 16g .. 16g+15) of its row, so the 4 lane groups cover one 128-byte line per row.
-//    MFMA step s (of 2) uses K = 16g + 8s + 0..7; the B fragments are read from LDS with
-//    the same K order, so the product is the plain dot product.
-//  * Each wave holds 64 x BN f32 accumulators (4 x BN/16 blocks of 16x16).
+// Warp-specialised workgroup: MW "math" wave64s + MW "producer" wave64s.  Waves are dealt
+// to the CU's four SIMDs round-robin, so with MW = 4 every SIMD runs one math wave and one
+// producer wave: the producer's global loads and nibble unpacking (VALU) issue while the
+// math wave's MFMAs occupy the matrix core.
+//  * Tile: BM = 64*MW tokens x BN weight rows (BN = 128 or 64), K stepped by 64 (one Q4_K
+//    chunk = sub-blocks 2c and 2c+1 of each weight row).
+//  * Producers: per K step, read each weight row's 16-byte Q4_K header (d, dmin, 12 scale
+//    bytes) and 32 bytes of nibbles, dequantize with f32 scale/min math (one rounding to
+//    f16 per value) and write the BN x 64 f16 stage into LDS (double-buffered).  The raw
+//    bytes of step k+2 are in flight while step k+1 is unpacked.
+//  * Math waves: each owns 64 token rows, streams them straight from global memory into
+//    VGPRs one step ahead.  Activations are stored in MFMA operand order (tiled_index), so
+//    each 16-row x 32-column operand is one contiguous 1 KiB dwordx4 load per wave.  They
+//    run 4 x BN/16 MFMAs per 32-wide K slice with the weight fragment as the A operand:
+//    D^T = W . X^T, so each lane ends up with 4 consecutive output columns of one token and
+//    the epilogue stores 8-16 bytes at a time (f16 outputs that feed the next GEMM are
+//    written in operand order too).
+//  * One barrier per K step hands the LDS stage from producers to math waves.
 //  * Tiles are ordered so that each XCD (8 per device, workgroups dealt round-robin) works
 //    on a contiguous band of M tiles: its L2 holds the A rows it streams plus the weights.
 #include "common.hpp"
 
 namespace {
 
-constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 reads
+constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 fragment reads
 
 __device__ __forceinline__ int sbyte(const uint4& hd, int i) {
   // byte i (0..11) of the 12 packed scale bytes = header bytes 4..15
@@ -31,7 +36,7 @@ __device__ __forceinline__ int sbyte(const uint4& hd, int i) {
   return (int)((w >> (8 * (i & 3))) & 0xff);
 }
 
-// GGML get_scale_min_k4 for the chunk pair (2c, 2c+1); c is wave-uniform.
+// GGML get_scale_min_k4 for the sub-block pair (2c, 2c+1); c is wave-uniform.
 __device__ __forceinline__ void chunk_scales(const uint4& hd, int c, float& s0, float& o0, float& s1,
                                              float& o1) {
   const float d = f16_bits_to_f32(hd.x & 0xffff), dmin = f16_bits_to_f32(hd.x >> 16);
@@ -54,7 +59,7 @@ __device__ __forceinline__ void chunk_scales(const uint4& hd, int c, float& s0, 
   o1 = dmin * (float)m1;
 }
 
-// Dequantize 4 packed bytes (8 nibbles) -> 4 low-nibble and 4 high-nibble f16 values.
+// 4 packed bytes (8 nibbles) -> 4 low-nibble (sub-block 2c) and 4 high-nibble (2c+1) f16.
 __device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, float o1, h4& lo, h4& hi) {
   const uint32_t l = v & 0x0f0f0f0fu, h = (v >> 4) & 0x0f0f0f0fu;
   lo = h4{(_Float16)(s0 * (float)(l & 0xff) - o0), (_Float16)(s0 * (float)((l >> 8) & 0xff) - o0),
@@ -63,9 +68,12 @@ __device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, f
           (_Float16)(s1 * (float)((h >> 16) & 0xff) - o1), (_Float16)(s1 * (float)(h >> 24) - o1)};
 }
 
+// B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns
+// n0.., rows [BN/2, BN) the same W1 columns, so a math wave's N blocks nb < NB/2 (gate)
+// and nb + NB/2 (up) hold the same output columns in the same lanes.
 template <int EPI, int BN>
 __device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const void*& W, int& n) {
-  if (EPI == EPI_GATED) {  // rows [0,BN/2): W0 columns n0.., rows [BN/2,BN): W1 same columns
+  if (EPI == EPI_GATED) {
     W = r < BN / 2 ? p.W0 : p.W1;
     n = n0 + (r & (BN / 2 - 1));
   } else {
@@ -74,22 +82,23 @@ __device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const voi
   }
 }
 
-// Raw B data of one K step held in registers between the global load and the LDS store.
-template <int WF, int NT, int BN>
+// Raw weights of one K step held by a producer thread between load and unpack.
+template <int WF, int NP, int BN>
 struct BRaw {
-  static constexpr int TPR = NT / BN;           // threads per weight row (Q4_K)
-  static constexpr int BPT = 32 / TPR;          // nibble bytes per thread
-  static constexpr int F16_LOADS = BN * BK * 2 / 16 / NT;
+  static constexpr int TPR = NP / BN;   // producer threads per weight row (Q4_K)
+  static constexpr int BPT = 32 / TPR;  // nibble bytes per thread: 32, 16 or 8
+  static constexpr int NQ = BPT / 4;
+  static constexpr int F16_LOADS = BN * BK * 2 / 16 / NP;
   uint4 hd;
-  uint32_t q[BPT / 4];
+  uint32_t q[NQ];
   uint4 f[WF == WF_F16 ? F16_LOADS : 1];
 };
 
-template <int EPI, int WF, int NT, int BN>
-__device__ __forceinline__ void load_b(BRaw<WF, NT, BN>& br, const GemmArgs& p, int n0, int kt, int tid) {
-  using R = BRaw<WF, NT, BN>;
-  if (WF == WF_Q4K) {
-    const int r = tid / R::TPR, part = tid % R::TPR;
+template <int EPI, int WF, int NP, int BN>
+__device__ __forceinline__ void load_b(BRaw<WF, NP, BN>& br, const GemmArgs& p, int n0, int kt, int pt) {
+  using R = BRaw<WF, NP, BN>;
+  if constexpr (WF == WF_Q4K) {
+    const int r = pt / R::TPR, part = pt % R::TPR;
     const void* W;
     int n;
     brow<EPI, BN>(r, n0, p, W, n);
@@ -111,7 +120,7 @@ __device__ __forceinline__ void load_b(BRaw<WF, NT, BN>& br, const GemmArgs& p, 
   } else {
 #pragma unroll
     for (int i = 0; i < R::F16_LOADS; i++) {
-      const int idx = i * NT + tid, r = idx >> 3, c8 = (idx & 7) * 8;
+      const int idx = i * NP + pt, r = idx >> 3, c8 = (idx & 7) * 8;
       const void* W;
       int n;
       brow<EPI, BN>(r, n0, p, W, n);
@@ -120,34 +129,39 @@ __device__ __forceinline__ void load_b(BRaw<WF, NT, BN>& br, const GemmArgs& p, 
   }
 }
 
-template <int WF, int NT, int BN>
-__device__ __forceinline__ void store_b(const BRaw<WF, NT, BN>& br, _Float16* Bs, int kt, int tid) {
-  using R = BRaw<WF, NT, BN>;
-  if (WF == WF_Q4K) {
-    const int r = tid / R::TPR, part = tid % R::TPR;
+template <int WF, int NP, int BN>
+__device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs, int kt, int pt) {
+  using R = BRaw<WF, NP, BN>;
+  if constexpr (WF == WF_Q4K) {
+    const int r = pt / R::TPR, part = pt % R::TPR;
     const int c = ((kt * BK) % QK_K) / 64;
     float s0, o0, s1, o1;
     chunk_scales(br.hd, c, s0, o0, s1, o1);
     _Float16* row = Bs + r * LDSK;
 #pragma unroll
-    for (int w = 0; w < R::BPT / 4; w++) {
-      h4 lo, hi;
-      deq4(br.q[w], s0, o0, s1, o1, lo, hi);
-      *reinterpret_cast<h4*>(row + part * R::BPT + 4 * w) = lo;
-      *reinterpret_cast<h4*>(row + 32 + part * R::BPT + 4 * w) = hi;
+    for (int w = 0; w < R::NQ; w += 2) {
+      h4 lo0, hi0, lo1, hi1;
+      deq4(br.q[w], s0, o0, s1, o1, lo0, hi0);
+      deq4(br.q[w + 1], s0, o0, s1, o1, lo1, hi1);
+      *reinterpret_cast<h8*>(row + part * R::BPT + 4 * w) =
+          h8{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+      *reinterpret_cast<h8*>(row + 32 + part * R::BPT + 4 * w) =
+          h8{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
     }
   } else {
 #pragma unroll
     for (int i = 0; i < R::F16_LOADS; i++) {
-      const int idx = i * NT + tid, r = idx >> 3, c8 = (idx & 7) * 8;
+      const int idx = i * NP + pt, r = idx >> 3, c8 = (idx & 7) * 8;
       *reinterpret_cast<uint4*>(Bs + r * LDSK + c8) = br.f[i];
     }
   }
 }
 
 template <int EPI, int WF, int MW, int BN>
-__global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
-  constexpr int NT = 64 * MW, BM = 64 * MW, NB = BN / 16;
+__global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+  constexpr int NP = 64 * MW, BM = 64 * MW, NB = BN / 16;
+  using R = BRaw<WF, NP, BN>;
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
 
   // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous tile range.
@@ -155,16 +169,38 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (tile >= tiles_m * tiles_n) return;
   const int tm = tile / tiles_n, tn = tile % tiles_n;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 15, lg = lane >> 4;
   const int m0 = tm * BM;
   const int n0 = tn * (EPI == EPI_GATED ? BN / 2 : BN);
   const int nkt = p.K / BK;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // waves [0, MW) compute, waves [MW, 2MW) produce; wave w runs on SIMD w % 4
 
-  const _Float16* arow[4];
+  if (wave >= MW) {
+    // ------------------------------ producer waves ------------------------------
+    const int pt = tid - NP;
+    R br;
+    load_b<EPI, WF, NP, BN>(br, p, n0, 0, pt);
+    store_b<WF, NP, BN>(br, Bs[0], 0, pt);
+    if (nkt > 1) load_b<EPI, WF, NP, BN>(br, p, n0, 1, pt);
+    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int kt = 0; kt < nkt; kt++) {
+      // unpack step kt+1 (its raw bytes were loaded one step earlier), then fetch kt+2;
+      // the barrier count matches the math waves' loop exactly
+      if (kt + 1 < nkt) store_b<WF, NP, BN>(br, Bs[(kt + 1) & 1], kt + 1, pt);
+      if (kt + 2 < nkt) load_b<EPI, WF, NP, BN>(br, p, n0, kt + 2, pt);
+      __syncthreads();
+    }
+    return;
+  }
+
+  // -------------------------------- math waves ---------------------------------
+  const int lr = lane & 15, lg = lane >> 4;
+  // operand blocks of this wave's 4 row groups: block (rb, kb) at ((rb * K/32) + kb) * 512
+  const size_t kblk = p.K / 32;
+  const _Float16* ablk[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++) arow[mb] = p.A + (size_t)(m0 + wave * 64 + mb * 16 + lr) * p.lda + 16 * lg;
+  for (int mb = 0; mb < 4; mb++) ablk[mb] = p.A + ((size_t)((m0 + wave * 64) / 16 + mb) * kblk) * 512 + lane * 8;
 
   f4 acc[4][NB];
 #pragma unroll
@@ -173,45 +209,32 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   uint4 a0[4][2], a1[4][2];
-  BRaw<WF, NT, BN> br;
-
 #define LOAD_A(dst, kt)                                                                     \
   _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                        \
-    dst[mb][0] = *reinterpret_cast<const uint4*>(arow[mb] + (kt) * BK);                     \
-    dst[mb][1] = *reinterpret_cast<const uint4*>(arow[mb] + (kt) * BK + 8);                 \
+    dst[mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);       \
+    dst[mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512);   \
   }
-#define COMPUTE(areg, buf)                                                                  \
-  _Pragma("unroll") for (int s = 0; s < 2; s++) {                                           \
-    h8 bf[NB];                                                                              \
-    _Pragma("unroll") for (int nb = 0; nb < NB; nb++) bf[nb] =                              \
-        *reinterpret_cast<const h8*>(&Bs[buf][(nb * 16 + lr) * LDSK + 16 * lg + 8 * s]);    \
-    _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                      \
-      const h8 af = __builtin_bit_cast(h8, areg[mb][s]);                                    \
-      _Pragma("unroll") for (int nb = 0; nb < NB; nb++) acc[mb][nb] =                       \
-          __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);         \
-    }                                                                                       \
-  }
-
-  load_b<EPI, WF, NT, BN>(br, p, n0, 0, tid);
   LOAD_A(a0, 0);
-  store_b<WF, NT, BN>(br, Bs[0], 0, tid);
   __syncthreads();
-  // Drain every counter once here: otherwise the prologue's A loads are still pending at
-  // the loop header, and the wait that covers them lands inside the loop body, where in
-  // steady state it would stall each step on the *next* step's prefetch.
   __builtin_amdgcn_s_waitcnt(0);
 
-  // One MFMA site per iteration keeps the accumulators in place (no AGPR<->VGPR copies);
-  // the next step's A and B are in flight while this step's MFMAs run.
+  const _Float16* bbase = &Bs[0][lr * LDSK + 8 * lg];
   for (int kt = 0; kt < nkt; kt++) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nkt;
-    if (more) {  // B first: store_b below then waits only for the B loads
-      load_b<EPI, WF, NT, BN>(br, p, n0, kt + 1, tid);
-      LOAD_A(a1, kt + 1);
+    if (kt + 1 < nkt) LOAD_A(a1, kt + 1);
+    const _Float16* bsrc = bbase + (kt & 1) * (BN * LDSK);
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      h8 wf[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) wf[nb] = *reinterpret_cast<const h8*>(bsrc + nb * 16 * LDSK + 32 * s);
+#pragma unroll
+      for (int mb = 0; mb < 4; mb++) {
+        const h8 xf = __builtin_bit_cast(h8, a0[mb][s]);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[nb], xf, acc[mb][nb], 0, 0, 0);
+      }
     }
-    COMPUTE(a0, buf);
-    if (more) store_b<WF, NT, BN>(br, Bs[buf ^ 1], kt + 1, tid);
     __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) {
@@ -220,51 +243,57 @@ __global__ __launch_bounds__(64 * MW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   }
 #undef LOAD_A
-#undef COMPUTE
 
-  // ---- epilogue: lane holds D[row 4*lg+i][col lr] of each 16x16 block ----
-  const int rbase = m0 + wave * 64 + lg * 4;
-  if (EPI == EPI_GATED) {
-    _Float16* out = (_Float16*)p.out;
+  // ---- epilogue: lane holds C[token m0+64w+16mb+lr][columns n0+16nb+4lg+0..3] ----
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++)
+  for (int mb = 0; mb < 4; mb++) {
+    const int m = m0 + wave * 64 + mb * 16 + lr;
+    if (m >= p.M) continue;
+    if constexpr (EPI == EPI_GATED) {  // hidden state in operand order for the wo GEMM
 #pragma unroll
       for (int nb = 0; nb < NB / 2; nb++) {
-        const int n = n0 + nb * 16 + lr;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int m = rbase + mb * 16 + i;
-          if (m < p.M) out[(size_t)m * p.ldo + n] = (_Float16)(gelu_tanh_dev(acc[mb][nb][i]) * acc[mb][nb + NB / 2][i]);
-        }
+        const f4 g = acc[mb][nb], u = acc[mb][nb + NB / 2];
+        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
+            h4{(_Float16)(gelu_tanh_dev(g[0]) * u[0]), (_Float16)(gelu_tanh_dev(g[1]) * u[1]),
+               (_Float16)(gelu_tanh_dev(g[2]) * u[2]), (_Float16)(gelu_tanh_dev(g[3]) * u[3])};
       }
-  } else {
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++)
+    } else if constexpr (EPI == EPI_RESID) {
+      float* xrow = (float*)p.out + (size_t)m * p.ldo + n0 + 4 * lg;
 #pragma unroll
       for (int nb = 0; nb < NB; nb++) {
-        const int n = n0 + nb * 16 + lr;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int m = rbase + mb * 16 + i;
-          if (m >= p.M) continue;
-          const float v = acc[mb][nb][i];
-          if (EPI == EPI_F16) {
-            ((_Float16*)p.out)[(size_t)m * p.ldo + n] = (_Float16)v;
-          } else if (EPI == EPI_RELU) {
-            ((_Float16*)p.out)[(size_t)m * p.ldo + n] = (_Float16)(v > 0.f ? v : 0.f);
-          } else if (EPI == EPI_F32) {
-            ((float*)p.out)[(size_t)m * p.ldo + n] = v;
-          } else if (EPI == EPI_RESID) {
-            float* x = (float*)p.out + (size_t)m * p.ldo + n;
-            *x = *x + v;
-          } else {  // EPI_QKV
-            const int nn = n + p.n_off, inner = p.heads * p.dkv;
-            const int which = nn / inner, rem = nn % inner;
-            const int h = rem / p.dkv, d = rem % p.dkv;
-            ((_Float16*)p.out)[(((size_t)which * p.heads + h) * p.tpad + m) * p.dkv + d] = (_Float16)v;
-          }
-        }
+        float4 x = *reinterpret_cast<float4*>(xrow + nb * 16);
+        x.x += acc[mb][nb][0];
+        x.y += acc[mb][nb][1];
+        x.z += acc[mb][nb][2];
+        x.w += acc[mb][nb][3];
+        *reinterpret_cast<float4*>(xrow + nb * 16) = x;
       }
+    } else if constexpr (EPI == EPI_F32) {
+      float* orow = (float*)p.out + (size_t)m * p.ldo + n0 + 4 * lg;
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++)
+        *reinterpret_cast<float4*>(orow + nb * 16) =
+            make_float4(acc[mb][nb][0], acc[mb][nb][1], acc[mb][nb][2], acc[mb][nb][3]);
+    } else if constexpr (EPI == EPI_F16 || EPI == EPI_RELU) {  // operand order for the next GEMM
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        f4 v = acc[mb][nb];
+        if (EPI == EPI_RELU) v = f4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
+        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
+            h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+      }
+    } else {  // EPI_QKV: 4 consecutive columns stay inside one head (dkv % 4 == 0)
+      const int inner = p.heads * p.dkv;
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        const int nn = n0 + nb * 16 + 4 * lg + p.n_off;
+        const int which = nn / inner, rem = nn % inner;
+        const int h = rem / p.dkv, d = rem % p.dkv;
+        _Float16* dst = (_Float16*)p.out + (((size_t)which * p.heads + h) * p.tpad + m) * p.dkv + d;
+        *reinterpret_cast<h4*>(dst) = h4{(_Float16)acc[mb][nb][0], (_Float16)acc[mb][nb][1],
+                                         (_Float16)acc[mb][nb][2], (_Float16)acc[mb][nb][3]};
+      }
+    }
   }
 }
 
@@ -273,11 +302,10 @@ hipError_t launch_cfg(int mw, const GemmArgs& a, hipStream_t s) {
   const int cols = EPI == EPI_GATED ? BN / 2 : BN;
   const int tiles_n = a.N / cols, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
   const int grid = (tiles_m * tiles_n + 7) / 8 * 8;
-  switch (mw) {
-    case 2: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN>), dim3(grid), dim3(128), 0, s, a, tiles_m, tiles_n); break;
-    case 4: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n); break;
-    default: hipLaunchKernelGGL((gemm_kernel<EPI, WF, 8, BN>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n); break;
-  }
+  if (mw == 2)
+    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -291,12 +319,11 @@ hipError_t launch_epi(int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s
 }  // namespace
 
 namespace t5k {
-// Tile choice for C[M, N]: rows 64*mw (mw in {2, 4, 8}) x bn weight rows (64 or 128).
-// Measured on MI355X for every encoder GEMM (N = 128..4096, K = 768/2048, M = 32..73728):
-// the 4-wave x 128-row tile is fastest once it yields >= 1.4 tiles per CU; below that the
-// 4-wave x 64-row tile while it still covers >= 0.75 of the CUs; otherwise 2-wave x 64-row
-// tiles (small token counts, where latency dominates).  n_rows = weight rows of the launch
-// (both matrices for the gated FFN).
+// Tile choice for C[M, N]: 64*mw token rows (mw in {2, 4}) x bn weight rows (64 or 128).
+// Prefer the 4-math-wave x 128-row tile once it yields >= 1.4 tiles per CU; then the
+// 4 x 64 tile while it still covers >= 0.75 of the CUs; otherwise 2 x 64 (small token
+// counts, where latency dominates).  n_rows = weight rows of the launch (both matrices
+// for the gated FFN).
 void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn) {
   auto tiles = [&](int w, int b) { return (double)((M + 64 * w - 1) / (64 * w)) * (n_rows / b); };
   if (n_rows % 128 == 0 && tiles(4, 128) >= 1.4 * cus) {
@@ -313,6 +340,7 @@ void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn) {
 
 hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
+  if (mw != 2 && mw != 4) mw = 4;
   switch (epi) {
     case EPI_F16: return launch_epi<EPI_F16>(wfmt, mw, bn, a, s);
     case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, mw, bn, a, s);

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 }
 
 // T5LayerNorm (src/quantized_t5.rs:162-173): x / sqrt(mean(x^2) + eps) * w, emitted as the
-// f16 GEMM operand.  One wave per row.
+// f16 GEMM operand (operand order, see tiled_index).  One wave per row.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       _Float16* __restrict__ out, int T, int D,
@@ -71,11 +71,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   ss = wave_sum(ss);
   const float den = sqrtf(ss / (float)D + eps);
   const float4* wr = reinterpret_cast<const float4*>(w);
-  h4* orow = reinterpret_cast<h4*>(out + (size_t)t * D);
   for (int i = lane; i < D / 4; i += 64) {
     const float4 v = xr[i], g = wr[i];
-    orow[i] = h4{(_Float16)((v.x / den) * g.x), (_Float16)((v.y / den) * g.y),
-                 (_Float16)((v.z / den) * g.z), (_Float16)((v.w / den) * g.w)};
+    *reinterpret_cast<h4*>(out + tiled_index(t, 4 * i, D)) =
+        h4{(_Float16)((v.x / den) * g.x), (_Float16)((v.y / den) * g.y), (_Float16)((v.z / den) * g.z),
+           (_Float16)((v.w / den) * g.w)};
   }
 }
 
@@ -95,9 +95,10 @@ __global__ __launch_bounds__(256) void rownorm_kernel(float* __restrict__ y, flo
     for (int i = lane; i < P; i += 64) r[i] = r[i] / n;
 }
 
-__global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restrict__ y, size_t n) {
+// f32 [T][K] row-major -> f16 GEMM operand (operand order).
+__global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restrict__ y, size_t n, int K) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = (_Float16)x[i];
+  if (i < n) y[tiled_index(i / K, i % K, K)] = (_Float16)x[i];
 }
 
 // Embedder window summation (src/embedder.rs:38-63): token t's row is the sum, in window
@@ -147,9 +148,9 @@ hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hi
   hipLaunchKernelGGL(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize);
   return hipGetLastError();
 }
-hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, hipStream_t s) {
+hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, K);
   return hipGetLastError();
 }
 hipError_t launch_window_sum(const float* win, const int* src, int n, int maxw, int P, float* sum,

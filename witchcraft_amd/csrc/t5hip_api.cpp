@@ -889,7 +889,7 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   const Layer& Ly = m->layers[layer];
   const size_t bytes = (size_t)T * c.d_model * 4;
   HIP_OK(hipMemcpyAsync(m->x, x, bytes, hipMemcpyHostToDevice, m->stream));
-  HIP_OK(t5k::launch_f32_to_f16(m->x, m->xn, (size_t)T * c.d_model, m->stream));
+  HIP_OK(t5k::launch_f32_to_f16(m->x, m->xn, (size_t)T * c.d_model, c.d_model, m->stream));
   if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, c.d_model, T, m->hb, c.d_ff))) return rc;
   if ((rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, c.d_model))) return rc;
   HIP_OK(hipMemcpyAsync(y, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
