@@ -54,8 +54,8 @@ struct AttnArgs {
   _Float16* out;        // [T][H*dkv] in operand order (tiled_index)
   const int* cu;        // [B+1] device
   const int2* work;     // (seq, q_tile) pairs
-  const float* lut;     // [H][2*maxl-1] relative bias by (j - i)
-  int heads, tpad, maxl;
+  const float* lut;     // [H][2*lutw+1] relative bias by (j - i), centred at lutw
+  int heads, tpad, lutw;
 };
 
 // Device-side helpers ---------------------------------------------------------
@@ -70,10 +70,9 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
 // candle Tensor::gelu (tanh form): 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
 // evaluated as the identical x * sigmoid(2u) = x / (1 + 2^(-2u log2 e)).
 __device__ __forceinline__ float gelu_tanh_dev(float x) {
-  const float x2 = x * x;
-  const float u = x * (0.7978845608028654f + 0.0356774081363001f * x2);
-  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
+  // -2 log2(e) * u = x * (-2.302208198 - 0.102943497 x^2)
+  const float t = x * __builtin_fmaf(-0.10294324148f * x, x, -2.3022081983f);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // Host-side launchers (defined in the .hip files) --------------------------------

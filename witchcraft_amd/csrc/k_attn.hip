@@ -9,10 +9,15 @@
 // materialising [H, L, L].
 //
 // Workgroup = 4 wave64s = 64 queries of one (sequence, head); each wave owns 16 queries.
-// Keys are streamed in tiles of 64 through LDS (K row-major, V transposed) with an
-// online softmax.  The score block is computed transposed, S^T = K . Q^T, so that the
-// accumulator layout (lane = query column, 4 consecutive keys per lane group) is exactly
-// the B-operand layout the P.V MFMA needs: P never leaves registers.
+// Keys are streamed in tiles of 64 through double-buffered LDS with an online softmax; the
+// next tile's global loads are issued before the current tile is computed, so one barrier
+// per tile remains and load latency overlaps the MFMA/softmax work.  The score block is
+// computed transposed, S^T = K . Q^T, so that the accumulator layout (lane = query column,
+// 4 consecutive keys per lane group) is exactly the B-operand layout the P.V MFMA needs:
+// P never leaves registers.  V is transposed on its way into LDS (4x4 register blocks, 8-byte
+// stores) with the keys of each 32-key group permuted so that a lane's 8 P.V operand keys are
+// one contiguous 16-byte read.  The 127 bias values a tile needs (by j - i) are staged in LDS
+// with the tile.
 #include "common.hpp"
 
 namespace {
@@ -23,49 +28,81 @@ constexpr int DK = 64;   // head dim (d_kv)
 constexpr int KPAD = DK + 8;
 constexpr int VPAD = KT + 8;
 
+// Slot of key `key` (a multiple of 4) inside a tile row of Vt: key 16h + 4g + i of a 32-key
+// group sits at 8g + 4h + i, so keys {4g..4g+3, 16+4g..16+4g+3} -- the K-slots 8g..8g+7 of
+// the P^T operand built from the S^T accumulators -- are contiguous.
+__device__ __forceinline__ int vslot(int key) {
+  const int kk = key & 31;
+  return (key & ~31) + 8 * ((kk >> 2) & 3) + 4 * (kk >> 4);
+}
+
 __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[KT * KPAD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[DK * VPAD];
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KT * KPAD];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[2][DK * VPAD];
+  __shared__ float Bs[2][2 * KT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int2 wk = p.work[blockIdx.x];
-  const int seq = wk.x, qtile = wk.y, h = blockIdx.y;
+  const int2 wk = p.work[blockIdx.x / p.heads];
+  const int seq = wk.x, q0 = wk.y * QT, h = blockIdx.x % p.heads;
   const int s0 = p.cu[seq], L = p.cu[seq + 1] - s0;
   const int lr = lane & 15, lg = lane >> 4;
 
   const size_t head_stride = (size_t)p.tpad * DK;
-  const _Float16* Q = p.qkv + ((size_t)0 * p.heads + h) * head_stride;
-  const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + h) * head_stride;
-  const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + h) * head_stride;
-  const float* lut = p.lut + (size_t)h * (2 * p.maxl - 1) + (p.maxl - 1);
+  const _Float16* Q = p.qkv + ((size_t)0 * p.heads + h) * head_stride + (size_t)s0 * DK;
+  const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + h) * head_stride + (size_t)s0 * DK;
+  const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + h) * head_stride + (size_t)s0 * DK;
+  // bias of distance d = j - i at lut[d], |d| <= lutw (lutw >= padded sequence length + 1)
+  const float* lut = p.lut + (size_t)h * (2 * p.lutw + 1) + p.lutw;
 
   // This lane's query (relative to the sequence start).  Queries past L compute on
   // in-bounds padding rows and are never stored.
-  const int qi = qtile * QT + wave * 16 + lr;
+  const int qi = q0 + wave * 16 + lr;
   h8 qf[2];
-  {
-    const _Float16* qrow = Q + (size_t)(s0 + qi) * DK;
-    qf[0] = *reinterpret_cast<const h8*>(qrow + lg * 8);
-    qf[1] = *reinterpret_cast<const h8*>(qrow + 32 + lg * 8);
-  }
+  qf[0] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + lg * 8);
+  qf[1] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 32 + lg * 8);
+
+  // tile staging: K copied row-major (rows kr, kr + 32; 8 dims at kc); V as a 4x4 block
+  // (keys vk..vk+3, dims vd..vd+3), zeroed past L so padding rows cannot inject NaN into P.V.
+  const int kr = tid >> 3, kc = (tid & 7) * 8;
+  const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4;
+  uint4 kreg0, kreg1;
+  h4 vreg[4];
+  float breg = 0.f;
+  auto gload = [&](int k0) {
+    kreg0 = *reinterpret_cast<const uint4*>(Kg + (size_t)(k0 + kr) * DK + kc);
+    kreg1 = *reinterpret_cast<const uint4*>(Kg + (size_t)(k0 + kr + 32) * DK + kc);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const h4 v = *reinterpret_cast<const h4*>(Vg + (size_t)(k0 + vk + j) * DK + vd);
+      vreg[j] = (k0 + vk + j < L) ? v : h4{0, 0, 0, 0};
+    }
+    if (tid < 2 * KT) breg = lut[k0 - q0 - (QT - 1) + tid];
+  };
+  auto lstore = [&](int buf) {
+    *reinterpret_cast<uint4*>(&Ks[buf][kr * KPAD + kc]) = kreg0;
+    *reinterpret_cast<uint4*>(&Ks[buf][(kr + 32) * KPAD + kc]) = kreg1;
+    const int slot = vslot(vk);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *reinterpret_cast<h4*>(&Vt[buf][(vd + i) * VPAD + slot]) =
+          h4{vreg[0][i], vreg[1][i], vreg[2][i], vreg[3][i]};
+    if (tid < 2 * KT) Bs[buf][tid] = breg;
+  };
 
   float m_run = -INFINITY, l_run = 0.f;
   f4 o[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) o[i] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < L; k0 += KT) {
-    // cooperative tile load: 64 keys x 64 dims of K (row-major) and V (transposed)
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int r = it * 32 + (tid >> 3), c = (tid & 7) * 8;
-      const size_t g = (size_t)(s0 + k0 + r) * DK + c;
-      *reinterpret_cast<uint4*>(&Ks[r * KPAD + c]) = *reinterpret_cast<const uint4*>(Kg + g);
-      const h8 v = *reinterpret_cast<const h8*>(Vg + g);
-#pragma unroll
-      for (int e = 0; e < 8; e++) Vt[(c + e) * VPAD + r] = v[e];
-    }
-    __syncthreads();
+  const int ntile = (L + KT - 1) / KT;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  // Bs index of this lane's (key 4lg + i of key block 0, query qi): (j - qi) - (k0 - q0 - 63)
+  const int bofs = (QT - 1) - wave * 16 - lr + 4 * lg;
+  for (int t = 0; t < ntile; ++t) {
+    const int k0 = t * KT, buf = t & 1;
+    if (t + 1 < ntile) gload(k0 + KT);
 
     // S^T[key][query] for 4 key blocks of 16
     f4 s[4];
@@ -74,7 +111,7 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
       s[kb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < 2; ds++) {
-        const h8 a = *reinterpret_cast<const h8*>(&Ks[(kb * 16 + lr) * KPAD + ds * 32 + lg * 8]);
+        const h8 a = *reinterpret_cast<const h8*>(&Ks[buf][(kb * 16 + lr) * KPAD + ds * 32 + lg * 8]);
         s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
       }
     }
@@ -85,11 +122,9 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int j = k0 + kb * 16 + lg * 4 + i;
-        const int dlt = min(max(j - qi, 1 - p.maxl), p.maxl - 1);  // clamp: padded rows only
-        float v = s[kb][i] + lut[dlt];
-        v = j < L ? v : -INFINITY;
-        s[kb][i] = v;
-        mx = fmaxf(mx, v);
+        const float v = s[kb][i] + Bs[buf][bofs + kb * 16 + i];
+        s[kb][i] = j < L ? v : -INFINITY;
+        mx = fmaxf(mx, s[kb][i]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -111,8 +146,8 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
 #pragma unroll
     for (int db = 0; db < 4; db++) o[db] *= corr;
 
-    // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; K-slot order = keys
-    // {16(2ks)+4lg+0..3, 16(2ks+1)+4lg+0..3} in both operands.
+    // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; K-slots 8lg..8lg+7 of step ks are
+    // keys {32ks + 4lg + 0..3, 32ks + 16 + 4lg + 0..3} in both operands.
     h8 pb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
@@ -122,16 +157,14 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
         pb[ks][4 + i] = (_Float16)s[2 * ks + 1][i];
       }
 #pragma unroll
-    for (int db = 0; db < 4; db++) {
+    for (int db = 0; db < 4; db++)
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
-        const _Float16* vrow = &Vt[(db * 16 + lr) * VPAD];
-        const h4 v0 = *reinterpret_cast<const h4*>(vrow + (2 * ks) * 16 + lg * 4);
-        const h4 v1 = *reinterpret_cast<const h4*>(vrow + (2 * ks + 1) * 16 + lg * 4);
-        const h8 a = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        const h8 a = *reinterpret_cast<const h8*>(&Vt[buf][(db * 16 + lr) * VPAD + ks * 32 + lg * 8]);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[ks], o[db], 0, 0, 0);
       }
-    }
+
+    if (t + 1 < ntile) lstore(buf ^ 1);
     __syncthreads();
   }
 
@@ -153,7 +186,9 @@ namespace t5k {
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s) {
   if (dkv != DK) return hipErrorInvalidValue;
   if (n_work <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_relbias_kernel, dim3(n_work, a.heads), dim3(256), 0, s, a);
+  // heads fastest: the work list is ordered longest sequence first, so the costliest
+  // workgroups start first on every head.
+  hipLaunchKernelGGL(attn_relbias_kernel, dim3((unsigned)n_work * a.heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 }  // namespace t5k

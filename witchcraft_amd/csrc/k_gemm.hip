@@ -59,13 +59,26 @@ __device__ __forceinline__ void chunk_scales(const uint4& hd, int c, float& s0, 
   o1 = dmin * (float)m1;
 }
 
-// 4 packed bytes (8 nibbles) -> 4 low-nibble (sub-block 2c) and 4 high-nibble (2c+1) f16.
+// Byte i of v as f32 (v_cvt_f32_ubyte{0..3}: extraction and conversion in one instruction).
+template <int I>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+  float r;
+  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// 4 packed bytes (8 nibbles) -> 4 low-nibble (sub-block 2c) and 4 high-nibble (2c+1) f16:
+// mask the nibbles into byte lanes once, convert each byte with one instruction, then one
+// fused multiply-add per value rounded once to f16.
 __device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, float o1, h4& lo, h4& hi) {
   const uint32_t l = v & 0x0f0f0f0fu, h = (v >> 4) & 0x0f0f0f0fu;
-  lo = h4{(_Float16)(s0 * (float)(l & 0xff) - o0), (_Float16)(s0 * (float)((l >> 8) & 0xff) - o0),
-          (_Float16)(s0 * (float)((l >> 16) & 0xff) - o0), (_Float16)(s0 * (float)(l >> 24) - o0)};
-  hi = h4{(_Float16)(s1 * (float)(h & 0xff) - o1), (_Float16)(s1 * (float)((h >> 8) & 0xff) - o1),
-          (_Float16)(s1 * (float)((h >> 16) & 0xff) - o1), (_Float16)(s1 * (float)(h >> 24) - o1)};
+  lo = h4{(_Float16)__builtin_fmaf(s0, ubyte<0>(l), -o0), (_Float16)__builtin_fmaf(s0, ubyte<1>(l), -o0),
+          (_Float16)__builtin_fmaf(s0, ubyte<2>(l), -o0), (_Float16)__builtin_fmaf(s0, ubyte<3>(l), -o0)};
+  hi = h4{(_Float16)__builtin_fmaf(s1, ubyte<0>(h), -o1), (_Float16)__builtin_fmaf(s1, ubyte<1>(h), -o1),
+          (_Float16)__builtin_fmaf(s1, ubyte<2>(h), -o1), (_Float16)__builtin_fmaf(s1, ubyte<3>(h), -o1)};
 }
 
 // B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns

@@ -54,28 +54,69 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 }
 
 // T5LayerNorm (src/quantized_t5.rs:162-173): x / sqrt(mean(x^2) + eps) * w, emitted as the
-// f16 GEMM operand (operand order, see tiled_index).  One wave per row.
+// f16 GEMM operand (operand order, see tiled_index).  One workgroup per 16-row band: wave w
+// owns the 16x32 operand blocks w, w+4, ... of the band, so each lane reads 32 contiguous bytes
+// of its row per block and each block leaves as one contiguous 1 KiB store.  Up to RN_KEEP
+// blocks per wave stay in registers between the sum of squares and the store (D <= 1024 reads x
+// once).  Rows >= T of the last band are written as zeros.
+constexpr int RN_KEEP = 8;
+
+__device__ __forceinline__ float sq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       _Float16* __restrict__ out, int T, int D,
                                                       float eps) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int lane = threadIdx.x & 63;
-  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
+  __shared__ float part[4][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 15, c8 = (lane >> 4) * 8;
+  const int t = blockIdx.x * 16 + r;
+  const bool live = t < T;
+  const int nblk = D >> 5;
+  const float* xr = x + (size_t)(live ? t : 0) * D + c8;
+  float4 keep[RN_KEEP][2];
   float ss = 0.f;
-  for (int i = lane; i < D / 4; i += 64) {
-    const float4 v = xr[i];
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+  for (int j = 0; j < RN_KEEP; ++j) {
+    const int kb = wave + 4 * j;
+    keep[j][0] = keep[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live && kb < nblk) {
+      keep[j][0] = *reinterpret_cast<const float4*>(xr + kb * 32);
+      keep[j][1] = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
+      ss += sq4(keep[j][0]) + sq4(keep[j][1]);
+    }
   }
-  ss = wave_sum(ss);
-  const float den = sqrtf(ss / (float)D + eps);
-  const float4* wr = reinterpret_cast<const float4*>(w);
-  for (int i = lane; i < D / 4; i += 64) {
-    const float4 v = xr[i], g = wr[i];
-    *reinterpret_cast<h4*>(out + tiled_index(t, 4 * i, D)) =
-        h4{(_Float16)((v.x / den) * g.x), (_Float16)((v.y / den) * g.y), (_Float16)((v.z / den) * g.z),
-           (_Float16)((v.w / den) * g.w)};
+  for (int kb = wave + 4 * RN_KEEP; live && kb < nblk; kb += 4)
+    ss += sq4(*reinterpret_cast<const float4*>(xr + kb * 32)) +
+          sq4(*reinterpret_cast<const float4*>(xr + kb * 32 + 4));
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  if (lane < 16) part[wave][lane] = ss;
+  __syncthreads();
+  const float tot = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
+  const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+  _Float16* ob = out + (size_t)blockIdx.x * nblk * 512 + lane * 8;
+  auto emit = [&](int kb, float4 a, float4 b) {
+    const float4 ga = *reinterpret_cast<const float4*>(w + kb * 32 + c8);
+    const float4 gb = *reinterpret_cast<const float4*>(w + kb * 32 + c8 + 4);
+    h8 o = h8{(_Float16)((a.x * inv) * ga.x), (_Float16)((a.y * inv) * ga.y),
+              (_Float16)((a.z * inv) * ga.z), (_Float16)((a.w * inv) * ga.w),
+              (_Float16)((b.x * inv) * gb.x), (_Float16)((b.y * inv) * gb.y),
+              (_Float16)((b.z * inv) * gb.z), (_Float16)((b.w * inv) * gb.w)};
+    *reinterpret_cast<h8*>(ob + (size_t)kb * 512) = o;
+  };
+#pragma unroll
+  for (int j = 0; j < RN_KEEP; ++j) {
+    const int kb = wave + 4 * j;
+    if (kb < nblk) emit(kb, keep[j][0], keep[j][1]);
+  }
+  for (int kb = wave + 4 * RN_KEEP; kb < nblk; kb += 4) {
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (live) {
+      a = *reinterpret_cast<const float4*>(xr + kb * 32);
+      b = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
+    }
+    emit(kb, a, b);
   }
 }
 
@@ -140,7 +181,7 @@ hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, 
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
                           hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, out, T, D, eps);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps);
   return hipGetLastError();
 }
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s) {

@@ -89,7 +89,10 @@ struct t5h_model {
   size_t arena_bytes = 0;
   const void* emb = nullptr;
   int emb_fmt = EMB_F32;
-  const float* rel_lut = nullptr;  // [H][2*maxl-1]
+  const float* rel_lut = nullptr;  // [H][2*lutw+1], bias of distance j - i at lutw + j - i
+  int lutw = 0;
+  std::vector<int> order;  // host scratch: sequence order of the attention work list
+  double attn_flops = 0;   // QK^T + PV flops of one attention launch on the current batch, true tokens
   const float* final_ln = nullptr;
   std::vector<Layer> layers;
   Linear proj;
@@ -407,8 +410,16 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   int* hc = (int*)s.host;
   memcpy(hc, cu, (size_t)(B + 1) * 4);
   int2* hw = (int2*)((uint8_t*)s.host + wofs);
+  // Longest sequences first (every query tile of a sequence costs ceil(L/64) key tiles), so
+  // the attention grid drains with its cheapest workgroups.
+  m->order.resize(B);
+  for (int b = 0; b < B; b++) m->order[b] = b;
+  std::stable_sort(m->order.begin(), m->order.end(),
+                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
   int w = 0;
-  for (int b = 0; b < B; b++) {
+  m->attn_flops = 0;
+  for (int b : m->order) {
+    m->attn_flops += 4.0 * (double)(cu[b + 1] - cu[b]) * (cu[b + 1] - cu[b]) * m->cfg.d_kv * m->cfg.num_heads;
     const int L = cu[b + 1] - cu[b];
     for (int q = 0; q * 64 < L; q++) hw[w++] = make_int2(b, q);
   }
@@ -461,8 +472,8 @@ int run_block(t5h_model* m, int l, int T, int nwork) {
     a.lut = m->rel_lut;
     a.heads = c.num_heads;
     a.tpad = m->tpad;
-    a.maxl = c.max_seq_len;
-    Timed t(m, K_ATTN, 0, 0);
+    a.lutw = m->lutw;
+    Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
   }
   if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D))) return rc;
@@ -479,16 +490,6 @@ int run_block(t5h_model* m, int l, int T, int nwork) {
   return T5H_OK;
 }
 
-// Attention FLOPs (QK^T + PV) of one block over the batch, true tokens only.
-double attn_flops(const t5h_model* m, const int32_t* cu, int B) {
-  double f = 0;
-  for (int b = 0; b < B; b++) {
-    const double L = cu[b + 1] - cu[b];
-    f += 4.0 * L * L * m->cfg.d_kv * m->cfg.num_heads;
-  }
-  return f;
-}
-
 // Full forward from device ids; results in m->out / m->norm (or the given pointers).
 int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
                     float* d_norm, int normalize) {
@@ -501,14 +502,8 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
     HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag,
                              m->stream));
   }
-  const size_t first_attn = m->pending.size();
   for (int l = 0; l < c.num_layers; l++)
     if ((rc = run_block(m, l, T, nwork))) return rc;
-  if (m->prof) {
-    const double af = attn_flops(m, cu, B);
-    for (size_t i = first_attn; i < m->pending.size(); i++)
-      if (m->pending[i].kind == K_ATTN) m->pending[i].flops = af;
-  }
   {
     Timed t(m, K_RMSNORM, 0, (double)T * c.d_model * 6);
     HIP_OK(t5k::launch_rmsnorm(m->x, m->final_ln, m->xn, T, c.d_model, c.layer_norm_epsilon, m->stream));
@@ -631,16 +626,18 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   if (rb->type != t5h::GGML_F32 || rb->shape.size() != 2 ||
       (int)rb->rows() != cfg->relative_attention_num_buckets || (int)rb->cols() != H)
     return fail(T5H_ERR_FORMAT, "tensor " + rb_name + ": expected F32 [num_buckets, num_heads]");
-  const int maxl = cfg->max_seq_len, span = 2 * maxl - 1;
+  // The attention kernel reads distances up to the padded sequence length + 1 (64-key
+  // tiles), so the LUT covers |j - i| <= roundup(max_seq_len, 64) + 64.
+  const int lutw = (cfg->max_seq_len + 63) / 64 * 64 + 64, span = 2 * lutw + 1;
   const size_t lut_off = ha.add(nullptr, (size_t)H * span * 4);
   {
     float* lut = reinterpret_cast<float*>(ha.bytes.data() + lut_off);
     const float* tab = reinterpret_cast<const float*>(rb->data);
-    for (int dlt = -(maxl - 1); dlt <= maxl - 1; dlt++) {
+    for (int dlt = -lutw; dlt <= lutw; dlt++) {
       const uint32_t i = dlt < 0 ? (uint32_t)(-dlt) : 0u, j = dlt < 0 ? 0u : (uint32_t)dlt;
       const uint32_t b = rel_bucket(i, j, cfg->relative_attention_num_buckets,
                                     cfg->relative_attention_max_distance);
-      for (int h = 0; h < H; h++) lut[(size_t)h * span + dlt + maxl - 1] = tab[b * H + h];
+      for (int h = 0; h < H; h++) lut[(size_t)h * span + dlt + lutw] = tab[b * H + h];
     }
   }
   m->layers.resize(cfg->num_layers);
@@ -695,6 +692,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   auto bind = [&](Linear& L) { L.w = base + L.off; };
   m->emb = base + emb_off;
   m->rel_lut = (const float*)(base + lut_off);
+  m->lutw = lutw;
   m->final_ln = (const float*)(base + fln_off);
   for (auto& Ly : m->layers) {
     Ly.ln0 = (const float*)(base + Ly.ln0_off);
