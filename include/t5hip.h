@@ -110,7 +110,10 @@ int t5h_layer_forward(t5h_model* model, int32_t layer, const float* x_in,
                       const int32_t* cu_seqlens, int32_t B, float* x_out);
 
 /* T5DenseGatedActDense::forward alone (src/quantized_t5.rs:231-252) on host x[T, d_model]:
- * y = wo(gelu(x wi_0^T) * (x wi_1^T)).  mode 0: fused FFN kernel, 1: two-GEMM path. */
+ * y = wo(gelu(x wi_0^T) * (x wi_1^T)).  Both modes run gate and up as one dequant-GEMM whose
+ * epilogue applies gelu(gate) * up (the [T, d_ff] pre-activations never reach memory), then wo.
+ * mode 0: the production kernels (the small-token GEMV kernels for T <= 64, the batched
+ * MFMA GEMM above); mode 1: the batched GEMM at every T. */
 int t5h_ffn_block(t5h_model* model, int32_t layer, const float* x, int32_t T, float* y,
                   int32_t mode);
 

@@ -47,6 +47,11 @@ struct GemmArgs {
   int ldo;
   int n_off;  // column offset added before the QKV scatter
   int heads, dkv, tpad;
+  // GEMV only: when xf is set, the operand is T5LayerNorm(xf) computed in the kernel
+  // (xf f32 [M][K] row-major, gamma [K]) instead of A.
+  const float* xf;
+  const float* gamma;
+  float eps;
 };
 
 struct AttnArgs {
@@ -79,6 +84,9 @@ __device__ __forceinline__ float gelu_tanh_dev(float x) {
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
 hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s);
+// Small-M variant (M <= GEMV_MAX_M tokens), same arguments and results.
+constexpr int GEMV_MAX_M = 64;
+hipError_t launch_gemv(int epi, int wfmt, const GemmArgs& a, hipStream_t s);
 void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,

@@ -25,61 +25,12 @@
 //  * Tiles are ordered so that each XCD (8 per device, workgroups dealt round-robin) works
 //    on a contiguous band of M tiles: its L2 holds the A rows it streams plus the weights.
 #include "common.hpp"
+#include "epilogue.hpp"
+#include "q4k.hpp"
 
 namespace {
 
 constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 fragment reads
-
-__device__ __forceinline__ int sbyte(const uint4& hd, int i) {
-  // byte i (0..11) of the 12 packed scale bytes = header bytes 4..15
-  const uint32_t w = i < 4 ? hd.y : (i < 8 ? hd.z : hd.w);
-  return (int)((w >> (8 * (i & 3))) & 0xff);
-}
-
-// GGML get_scale_min_k4 for the sub-block pair (2c, 2c+1); c is wave-uniform.
-__device__ __forceinline__ void chunk_scales(const uint4& hd, int c, float& s0, float& o0, float& s1,
-                                             float& o1) {
-  const float d = f16_bits_to_f32(hd.x & 0xffff), dmin = f16_bits_to_f32(hd.x >> 16);
-  int sc0, m0, sc1, m1;
-  const int j0 = 2 * c, j1 = 2 * c + 1;
-  if (c < 2) {
-    sc0 = sbyte(hd, j0) & 63;
-    m0 = sbyte(hd, j0 + 4) & 63;
-    sc1 = sbyte(hd, j1) & 63;
-    m1 = sbyte(hd, j1 + 4) & 63;
-  } else {
-    sc0 = (sbyte(hd, j0 + 4) & 15) | ((sbyte(hd, j0 - 4) >> 6) << 4);
-    m0 = (sbyte(hd, j0 + 4) >> 4) | ((sbyte(hd, j0) >> 6) << 4);
-    sc1 = (sbyte(hd, j1 + 4) & 15) | ((sbyte(hd, j1 - 4) >> 6) << 4);
-    m1 = (sbyte(hd, j1 + 4) >> 4) | ((sbyte(hd, j1) >> 6) << 4);
-  }
-  s0 = d * (float)sc0;
-  o0 = dmin * (float)m0;
-  s1 = d * (float)sc1;
-  o1 = dmin * (float)m1;
-}
-
-// Byte i of v as f32 (v_cvt_f32_ubyte{0..3}: extraction and conversion in one instruction).
-template <int I>
-__device__ __forceinline__ float ubyte(uint32_t v) {
-  float r;
-  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-  return r;
-}
-
-// 4 packed bytes (8 nibbles) -> 4 low-nibble (sub-block 2c) and 4 high-nibble (2c+1) f16:
-// mask the nibbles into byte lanes once, convert each byte with one instruction, then one
-// fused multiply-add per value rounded once to f16.
-__device__ __forceinline__ void deq4(uint32_t v, float s0, float o0, float s1, float o1, h4& lo, h4& hi) {
-  const uint32_t l = v & 0x0f0f0f0fu, h = (v >> 4) & 0x0f0f0f0fu;
-  lo = h4{(_Float16)__builtin_fmaf(s0, ubyte<0>(l), -o0), (_Float16)__builtin_fmaf(s0, ubyte<1>(l), -o0),
-          (_Float16)__builtin_fmaf(s0, ubyte<2>(l), -o0), (_Float16)__builtin_fmaf(s0, ubyte<3>(l), -o0)};
-  hi = h4{(_Float16)__builtin_fmaf(s1, ubyte<0>(h), -o1), (_Float16)__builtin_fmaf(s1, ubyte<1>(h), -o1),
-          (_Float16)__builtin_fmaf(s1, ubyte<2>(h), -o1), (_Float16)__builtin_fmaf(s1, ubyte<3>(h), -o1)};
-}
 
 // B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns
 // n0.., rows [BN/2, BN) the same W1 columns, so a math wave's N blocks nb < NB/2 (gate)
@@ -262,50 +213,13 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
   for (int mb = 0; mb < 4; mb++) {
     const int m = m0 + wave * 64 + mb * 16 + lr;
     if (m >= p.M) continue;
-    if constexpr (EPI == EPI_GATED) {  // hidden state in operand order for the wo GEMM
+    if constexpr (EPI == EPI_GATED) {
 #pragma unroll
-      for (int nb = 0; nb < NB / 2; nb++) {
-        const f4 g = acc[mb][nb], u = acc[mb][nb + NB / 2];
-        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
-            h4{(_Float16)(gelu_tanh_dev(g[0]) * u[0]), (_Float16)(gelu_tanh_dev(g[1]) * u[1]),
-               (_Float16)(gelu_tanh_dev(g[2]) * u[2]), (_Float16)(gelu_tanh_dev(g[3]) * u[3])};
-      }
-    } else if constexpr (EPI == EPI_RESID) {
-      float* xrow = (float*)p.out + (size_t)m * p.ldo + n0 + 4 * lg;
+      for (int nb = 0; nb < NB / 2; nb++)
+        store_quad_gated(p, m, n0 + nb * 16 + 4 * lg, acc[mb][nb], acc[mb][nb + NB / 2]);
+    } else {
 #pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        float4 x = *reinterpret_cast<float4*>(xrow + nb * 16);
-        x.x += acc[mb][nb][0];
-        x.y += acc[mb][nb][1];
-        x.z += acc[mb][nb][2];
-        x.w += acc[mb][nb][3];
-        *reinterpret_cast<float4*>(xrow + nb * 16) = x;
-      }
-    } else if constexpr (EPI == EPI_F32) {
-      float* orow = (float*)p.out + (size_t)m * p.ldo + n0 + 4 * lg;
-#pragma unroll
-      for (int nb = 0; nb < NB; nb++)
-        *reinterpret_cast<float4*>(orow + nb * 16) =
-            make_float4(acc[mb][nb][0], acc[mb][nb][1], acc[mb][nb][2], acc[mb][nb][3]);
-    } else if constexpr (EPI == EPI_F16 || EPI == EPI_RELU) {  // operand order for the next GEMM
-#pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        f4 v = acc[mb][nb];
-        if (EPI == EPI_RELU) v = f4{fmaxf(v[0], 0.f), fmaxf(v[1], 0.f), fmaxf(v[2], 0.f), fmaxf(v[3], 0.f)};
-        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
-            h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-      }
-    } else {  // EPI_QKV: 4 consecutive columns stay inside one head (dkv % 4 == 0)
-      const int inner = p.heads * p.dkv;
-#pragma unroll
-      for (int nb = 0; nb < NB; nb++) {
-        const int nn = n0 + nb * 16 + 4 * lg + p.n_off;
-        const int which = nn / inner, rem = nn % inner;
-        const int h = rem / p.dkv, d = rem % p.dkv;
-        _Float16* dst = (_Float16*)p.out + (((size_t)which * p.heads + h) * p.tpad + m) * p.dkv + d;
-        *reinterpret_cast<h4*>(dst) = h4{(_Float16)acc[mb][nb][0], (_Float16)acc[mb][nb][1],
-                                         (_Float16)acc[mb][nb][2], (_Float16)acc[mb][nb][3]};
-      }
+      for (int nb = 0; nb < NB; nb++) store_quad<EPI>(p, m, n0 + nb * 16 + 4 * lg, acc[mb][nb]);
     }
   }
 }

@@ -82,6 +82,7 @@ struct t5h_model {
   int inner = 0;
   int cus = 256;          // compute units of the device
   int gemm_mw_override = 0;  // T5H_GEMM_MW / T5H_GEMM_BN tuning knobs (0 = heuristic)
+  bool batched_only = false;  // route every linear through the batched GEMM (t5h_ffn_block mode 1)
   int gemm_bn_override = 0;
 
   // ---- weights (one device arena) ----
@@ -359,8 +360,17 @@ void resolve_timings(t5h_model* m) {
 }
 
 // Launch sequence -----------------------------------------------------------------
+// Small token counts run the GEMV kernels (unless a tuning override or t5h_ffn_block mode 1
+// forces the batched GEMM).
+bool use_gemv(const t5h_model* m, int M) {
+  return M <= t5k::GEMV_MAX_M && !m->gemm_mw_override && !m->batched_only;
+}
+
+// C = A . W^T (+ epilogue).  norm_w: on the GEMV path the operand is T5LayerNorm(m->x) with
+// this weight, computed inside the kernel (A is then unused); callers pass it only when
+// use_gemv() holds.
 int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, const _Float16* A, int lda,
-         int M, void* out, int ldo, int n_off = 0) {
+         int M, void* out, int ldo, int n_off = 0, const float* norm_w = nullptr) {
   GemmArgs a{};
   a.A = A;
   a.lda = lda;
@@ -381,6 +391,16 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
                            (epi == EPI_RESID ? 2.0 : 1.0);
   const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
   Timed t(m, kind, flops, bytes);
+  if (use_gemv(m, M)) {
+    if (norm_w) {
+      a.xf = m->x;
+      a.gamma = norm_w;
+      a.eps = m->cfg.layer_norm_epsilon;
+    }
+    HIP_OK(t5k::launch_gemv(epi, W.fmt, a, m->stream));
+    return T5H_OK;
+  }
+  if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
   int mw, bn;
   t5k::gemm_pick_tile(M, W.N * (W1 ? 2 : 1), m->cus, mw, bn);
   if (m->gemm_mw_override) mw = m->gemm_mw_override;
@@ -447,21 +467,30 @@ int validate_cu(const t5h_model* m, const int32_t* cu, int B, int& T) {
   return T5H_OK;
 }
 
+// T5LayerNorm of the residual stream into the f16 operand buffer, unless the consuming GEMV
+// fuses it (returns the weight to pass to gemm() then, else nullptr).
+const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
+  rc = T5H_OK;
+  if (use_gemv(m, T)) return w;
+  Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
+  const hipError_t e = t5k::launch_rmsnorm(m->x, w, m->xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon, m->stream);
+  if (e != hipSuccess) rc = fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
+  return nullptr;
+}
+
 int run_block(t5h_model* m, int l, int T, int nwork) {
   const t5h_config& c = m->cfg;
   const Layer& Ly = m->layers[l];
   const int D = c.d_model, inner = m->inner;
   int rc;
-  {
-    Timed t(m, K_RMSNORM, 0, (double)T * D * 6);
-    HIP_OK(t5k::launch_rmsnorm(m->x, Ly.ln0, m->xn, T, D, c.layer_norm_epsilon, m->stream));
-  }
+  const float* nw0 = prenorm(m, Ly.ln0, T, rc);
+  if (rc) return rc;
   if (Ly.fused_qkv) {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0))) return rc;
   } else {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner, nw0))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner, nw0))) return rc;
   }
   {
     AttnArgs a{};
@@ -477,14 +506,12 @@ int run_block(t5h_model* m, int l, int T, int nwork) {
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
   }
   if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D))) return rc;
-  {
-    Timed t(m, K_RMSNORM, 0, (double)T * D * 6);
-    HIP_OK(t5k::launch_rmsnorm(m->x, Ly.ln1, m->xn, T, D, c.layer_norm_epsilon, m->stream));
-  }
+  const float* nw1 = prenorm(m, Ly.ln1, T, rc);
+  if (rc) return rc;
   if (c.feed_forward_gated) {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff))) return rc;
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff, 0, nw1))) return rc;
   } else {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff))) return rc;
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff, 0, nw1))) return rc;
   }
   if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, D))) return rc;
   return T5H_OK;
@@ -504,11 +531,9 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
   }
   for (int l = 0; l < c.num_layers; l++)
     if ((rc = run_block(m, l, T, nwork))) return rc;
-  {
-    Timed t(m, K_RMSNORM, 0, (double)T * c.d_model * 6);
-    HIP_OK(t5k::launch_rmsnorm(m->x, m->final_ln, m->xn, T, c.d_model, c.layer_norm_epsilon, m->stream));
-  }
-  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim)))
+  const float* nwf = prenorm(m, m->final_ln, T, rc);
+  if (rc) return rc;
+  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim, 0, nwf)))
     return rc;
   {
     Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
@@ -888,8 +913,11 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   const size_t bytes = (size_t)T * c.d_model * 4;
   HIP_OK(hipMemcpyAsync(m->x, x, bytes, hipMemcpyHostToDevice, m->stream));
   HIP_OK(t5k::launch_f32_to_f16(m->x, m->xn, (size_t)T * c.d_model, c.d_model, m->stream));
-  if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, c.d_model, T, m->hb, c.d_ff))) return rc;
-  if ((rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, c.d_model))) return rc;
+  m->batched_only = mode == 1;
+  rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, c.d_model, T, m->hb, c.d_ff);
+  if (!rc) rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, c.d_model);
+  m->batched_only = false;
+  if (rc) return rc;
   HIP_OK(hipMemcpyAsync(y, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
   return finish_sync(m);
 }
