@@ -80,6 +80,101 @@ def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_
                       f"median of 7 after 1 warmup; f32 dequantize-at-load path; CPU: {cpu}"}
 
 
+def query_bench(args) -> None:
+    """cfg3 (query regime): B = 1, L = 32 tokens, one forward per query, latency p50/p95 over
+    `--queries` queries (>= 1000).  With --rotate R (default 8) the
+    queries cycle over R independent model replicas (R x 47.8 MB of Q4_K weights > the 256 MB
+    MALL), so weights stream from HBM as in a cold query; --rotate 1 measures the warm case."""
+    import torch
+
+    from witchcraft_amd import synth
+    from witchcraft_amd.encoder import T5EncoderModel
+
+    cfg = dict(synth.XTR_BASE)
+    img = synth.make_model(cfg, seed=args.seed)
+    models = [T5EncoderModel.from_gguf(img, cfg, hip_device=0) for _ in range(args.rotate)]
+    L = 32
+    rng = np.random.default_rng(2000 + args.seed)
+    pool = rng.integers(1, cfg["vocab_size"], size=(64, L)).astype(np.int32)
+    cu = np.array([0, L], np.int32)
+    dev = torch.device("cuda:0")
+    d_ids = [torch.from_numpy(q).to(dev) for q in pool]
+    d_out = torch.empty((L, cfg["proj_dim"]), dtype=torch.float32, device=dev)
+    d_norm = torch.empty(L, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def query(i):
+        m = models[i % len(models)]
+        m.encode_device(d_ids[i % len(d_ids)].data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+        m.synchronize()
+
+    for i in range(max(args.warmup, 2 * len(models))):
+        query(i)
+    lat = np.empty(args.queries)
+    t_all = time.perf_counter()
+    for i in range(args.queries):
+        t = time.perf_counter()
+        query(i)
+        lat[i] = time.perf_counter() - t
+    wall = time.perf_counter() - t_all
+    p50, p95 = float(np.percentile(lat, 50) * 1e6), float(np.percentile(lat, 95) * 1e6)
+    log(f"[bench] cfg3: {args.queries} queries over {len(models)} replicas: p50 {p50:.1f} us, p95 {p95:.1f} us")
+
+    # per-kernel event timing (one replica, warm) -> dominant GEMV kernel vs HBM roofline
+    m = models[0]
+    m.set_profiling(True)
+    reps = 50
+    for i in range(reps):
+        query(0)
+    stats = m.kernel_stats()
+    m.set_profiling(False)
+    kernels = {}
+    for name, st in stats.items():
+        if st["launches"]:
+            kernels[name] = {"launches_per_query": st["launches"] / reps,
+                             "avg_us": st["total_ms"] / st["launches"] * 1e3}
+    gemv = {k: v for k, v in stats.items() if k.startswith("gemm_") and v["launches"]}
+    dom_name = max(gemv, key=lambda k: gemv[k]["total_ms"])
+    dom = gemv[dom_name]
+    avg_s = dom["total_ms"] / dom["launches"] * 1e-3
+    bytes_per_launch = dom["bytes"] / dom["launches"]
+    achieved = bytes_per_launch / avg_s / 1e9
+    q_bytes = 47_947_392  # Q4_K weights + embedding rows + bias table + output + ids per query
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        om = orc.OracleModel(img, cfg)
+        om.forward(pool[0].astype(np.uint32), acc64=False)
+        times = []
+        t0 = time.perf_counter()
+        for i in range(64):
+            t = time.perf_counter()
+            om.forward(pool[i].astype(np.uint32), acc64=False)
+            times.append(time.perf_counter() - t)
+            if time.perf_counter() - t0 > args.cpu_budget:
+                break
+        om.close()
+        med = sorted(times)[len(times) // 2]
+        base = {"value": med * 1e6, "unit": "us/query (p50)", "cores": threads, "kind": "port",
+                "sample": f"{len(times)} queries of 32 tokens, batch-1, f32 dequantize-at-load path"}
+    line = {
+        "metric": "XTR-base Q4_K query encode latency p50 (B=1, L=32)", "value": p50, "unit": "us",
+        "n_gpus": 1, "steps": args.queries, "warmup": args.warmup, "ms_per_step": p50 * 1e-3,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "cfg3: XTR-base Q4_K encoder, query regime: batch 1, 32 tokens",
+                   "global_batch": 1, "seq_len": L, "replicas_rotated": len(models),
+                   "p95_us": p95, "queries_per_s": args.queries / wall, "parallelism": "single GPU"},
+        "roofline": {"kernel": f"{dom_name} (Q4_K GEMV, M = 32)", "bound": "hbm", "achieved": achieved,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6,
+                     "query_bytes": q_bytes, "query_floor_us": q_bytes / PEAK_HBM_GBS / 1e3},
+        "cpu_baseline": base, "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,6 +184,8 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--queries", type=int, default=1000, help="cfg3: number of timed queries")
+    ap.add_argument("--rotate", type=int, default=8, help="cfg3: model replicas cycled (MALL defeat)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 10 times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -107,6 +204,10 @@ def main() -> None:
         print(f"bench.py: this build measures one GPU (got --gpus {args.gpus}); sequences are "
               "independent, so N GPUs would each run this workload on their own share.", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "cfg3":
+        query_bench(args)
+        return
 
     import torch
 

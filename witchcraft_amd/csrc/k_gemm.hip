@@ -30,7 +30,7 @@
 
 namespace {
 
-constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad: conflict-free b128 fragment reads
+constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad
 
 // B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns
 // n0.., rows [BN/2, BN) the same W1 columns, so a math wave's N blocks nb < NB/2 (gate)
@@ -121,10 +121,14 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
   }
 }
 
-template <int EPI, int WF, int MW, int BN>
+template <int EPI, int WF, int MW, int BN, int S>
 __global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
   constexpr int NP = 64 * MW, BM = 64 * MW, NB = BN / 16;
+  // S register stages of A (math waves) and PB of raw weights (producers): the loads of a
+  // step are issued S-1 (PB-1) steps before it is consumed, covering L2/MALL latency.
+  // K / 64 is a multiple of S and of PB.
+  constexpr int PB = 4;
   using R = BRaw<WF, NP, BN>;
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
 
@@ -141,19 +145,25 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
 
   if (wave >= MW) {
     // ------------------------------ producer waves ------------------------------
+    // Raw bytes of step j live in ring slot j % PB; step kt+1 is unpacked into LDS while
+    // steps kt+2 .. kt+PB are in flight.  One barrier per step, as in the math waves.
     const int pt = tid - NP;
-    R br;
-    load_b<EPI, WF, NP, BN>(br, p, n0, 0, pt);
-    store_b<WF, NP, BN>(br, Bs[0], 0, pt);
-    if (nkt > 1) load_b<EPI, WF, NP, BN>(br, p, n0, 1, pt);
+    R br[PB];
+    load_b<EPI, WF, NP, BN>(br[0], p, n0, 0, pt);
+    store_b<WF, NP, BN>(br[0], Bs[0], 0, pt);
+#pragma unroll
+    for (int i = 1; i < PB; i++) load_b<EPI, WF, NP, BN>(br[i], p, n0, i, pt);
     __syncthreads();
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int kt = 0; kt < nkt; kt++) {
-      // unpack step kt+1 (its raw bytes were loaded one step earlier), then fetch kt+2;
-      // the barrier count matches the math waves' loop exactly
-      if (kt + 1 < nkt) store_b<WF, NP, BN>(br, Bs[(kt + 1) & 1], kt + 1, pt);
-      if (kt + 2 < nkt) load_b<EPI, WF, NP, BN>(br, p, n0, kt + 2, pt);
-      __syncthreads();
+    // nkt % PB == 0 (K % 256 == 0); loads past the last step re-read it (in bounds, unused)
+    // so that every load is unconditional and the compiler's wait counts stay exact.
+    for (int kt0 = 0; kt0 < nkt; kt0 += PB) {
+#pragma unroll
+      for (int u = 0; u < PB; u++) {
+        const int kt = kt0 + u;
+        if (kt + 1 < nkt) store_b<WF, NP, BN>(br[(u + 1) % PB], Bs[(kt + 1) & 1], kt + 1, pt);
+        load_b<EPI, WF, NP, BN>(br[u], p, n0, min(kt + PB, nkt - 1), pt);
+        __syncthreads();
+      }
     }
     return;
   }
@@ -172,38 +182,42 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
 #pragma unroll
     for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 a0[4][2], a1[4][2];
-#define LOAD_A(dst, kt)                                                                     \
+  // A ring: step j in register stage j % S, loaded S-1 steps before it is used.
+  uint4 a[S][4][2];
+#define LOAD_A(st, kt)                                                                      \
   _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                        \
-    dst[mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);       \
-    dst[mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512);   \
+    a[st][mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);     \
+    a[st][mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512); \
   }
-  LOAD_A(a0, 0);
+#pragma unroll
+  for (int i = 0; i < S - 1; i++) {
+    LOAD_A(i, i);
+    __builtin_amdgcn_sched_barrier(0);  // stages issued in order
+  }
   __syncthreads();
-  __builtin_amdgcn_s_waitcnt(0);
 
+  // nkt % S == 0 (K % 256 == 0); as in the producers, loads past the end are clamped
   const _Float16* bbase = &Bs[0][lr * LDSK + 8 * lg];
-  for (int kt = 0; kt < nkt; kt++) {
-    if (kt + 1 < nkt) LOAD_A(a1, kt + 1);
-    const _Float16* bsrc = bbase + (kt & 1) * (BN * LDSK);
+  for (int kt0 = 0; kt0 < nkt; kt0 += S) {
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-      h8 wf[NB];
+    for (int u = 0; u < S; u++) {
+      const int kt = kt0 + u;
+      {
+        LOAD_A((u + S - 1) % S, min(kt + S - 1, nkt - 1));
+        __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's MFMAs
+        const _Float16* bsrc = bbase + (kt & 1) * (BN * LDSK);
 #pragma unroll
-      for (int nb = 0; nb < NB; nb++) wf[nb] = *reinterpret_cast<const h8*>(bsrc + nb * 16 * LDSK + 32 * s);
+        for (int s = 0; s < 2; s++)
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++) {
-        const h8 xf = __builtin_bit_cast(h8, a0[mb][s]);
+          for (int nb = 0; nb < NB; nb++) {  // one weight fragment live at a time
+            const h8 wf = *reinterpret_cast<const h8*>(bsrc + nb * 16 * LDSK + 32 * s);
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[nb], xf, acc[mb][nb], 0, 0, 0);
+            for (int mb = 0; mb < 4; mb++)
+              acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, __builtin_bit_cast(h8, a[u][mb][s]),
+                                                                    acc[mb][nb], 0, 0, 0);
+          }
+        __syncthreads();
       }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
-      a0[mb][0] = a1[mb][0];
-      a0[mb][1] = a1[mb][1];
     }
   }
 #undef LOAD_A
@@ -224,16 +238,23 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
   }
 }
 
-template <int EPI, int WF, int BN>
-hipError_t launch_cfg(int mw, const GemmArgs& a, hipStream_t s) {
+template <int EPI, int WF, int BN, int S>
+hipError_t launch_s(int mw, const GemmArgs& a, hipStream_t s) {
   const int cols = EPI == EPI_GATED ? BN / 2 : BN;
   const int tiles_n = a.N / cols, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
   const int grid = (tiles_m * tiles_n + 7) / 8 * 8;
   if (mw == 2)
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN, S>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n);
   else
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN, S>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n);
   return hipGetLastError();
+}
+
+// A prefetch depth 2 (one step ahead): deeper rings measured slower -- the A stream is
+// bound by L1/TA bandwidth, not latency, and more requests in flight only add contention.
+template <int EPI, int WF, int BN>
+hipError_t launch_cfg(int mw, const GemmArgs& a, hipStream_t s) {
+  return launch_s<EPI, WF, BN, 2>(mw, a, s);
 }
 
 template <int EPI>

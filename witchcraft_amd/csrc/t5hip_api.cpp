@@ -93,6 +93,8 @@ struct t5h_model {
   const float* rel_lut = nullptr;  // [H][2*lutw+1], bias of distance j - i at lutw + j - i
   int lutw = 0;
   std::vector<int> order;  // host scratch: sequence order of the attention work list
+  std::vector<int32_t> last_cu;  // cu_seqlens of the batch whose cu / work list are on the device
+  int last_B = -1;
   double attn_flops = 0;   // QK^T + PV flops of one attention launch on the current batch, true tokens
   const float* final_ln = nullptr;
   std::vector<Layer> layers;
@@ -113,6 +115,9 @@ struct t5h_model {
   uint32_t* ids = nullptr;
   int* cu = nullptr;
   int2* work = nullptr;
+  // Out-of-vocabulary flag in mapped pinned host memory: the embed kernel stores 1 through
+  // err_flag (its device address); the host reads err_host after the stream is synchronised.
+  unsigned* err_host = nullptr;
   unsigned* err_flag = nullptr;
 
   // ---- host staging ----
@@ -134,6 +139,7 @@ struct t5h_model {
       if (s.done) (void)hipEventDestroy(s.done);
     }
     if (io) (void)hipHostFree(io);
+    if (err_host) (void)hipHostFree(err_host);
     for (auto& p : pending) {
       (void)hipEventDestroy(p.a);
       (void)hipEventDestroy(p.b);
@@ -266,10 +272,10 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   const size_t o_ids = take((size_t)tpad * 4);
   const size_t o_cu = take((size_t)(capB + 1) * 4);
   const size_t o_work = take((size_t)capW * 8);
-  const size_t o_err = take(256);
   if (m->ws) {
     HIP_OK(hipStreamSynchronize(m->stream));
     HIP_OK(hipFree(m->ws));
+    m->last_B = -1;  // device cu_seqlens / work list are gone
     m->ws = nullptr;
   }
   if (hipMalloc(&m->ws, off) != hipSuccess) {
@@ -290,7 +296,6 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   m->ids = (uint32_t*)(base + o_ids);
   m->cu = (int*)(base + o_cu);
   m->work = (int2*)(base + o_work);
-  m->err_flag = (unsigned*)(base + o_err);
   m->cap_tokens = tpad - 128;
   m->cap_seqs = capB;
   m->cap_work = capW;
@@ -413,6 +418,10 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
 int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   nwork = 0;
   for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
+  // The same batch layout as the previous upload (e.g. a stream of equal-length queries):
+  // the device copies of cu_seqlens and the work list are still current.
+  if (B == m->last_B && std::equal(cu, cu + B + 1, m->last_cu.begin())) return T5H_OK;
+  m->last_B = -1;
   StagingSlot& s = m->slots[m->next_slot];
   m->next_slot = (m->next_slot + 1) % 4;
   if (s.used) HIP_OK(hipEventSynchronize(s.done));
@@ -447,6 +456,8 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   if (nwork) HIP_OK(hipMemcpyAsync(m->work, hw, (size_t)nwork * 8, hipMemcpyHostToDevice, m->stream));
   HIP_OK(hipEventRecord(s.done, m->stream));
   s.used = true;
+  m->last_cu.assign(cu, cu + B + 1);
+  m->last_B = B;
   return T5H_OK;
 }
 
@@ -551,13 +562,9 @@ int check_model(t5h_model* m) {
 int finish_sync(t5h_model* m) {
   HIP_OK(hipStreamSynchronize(m->stream));
   if (m->prof) resolve_timings(m);
-  unsigned flag = 0;
-  if (m->err_flag) {
-    HIP_OK(hipMemcpy(&flag, m->err_flag, 4, hipMemcpyDeviceToHost));
-    if (flag) {
-      HIP_OK(hipMemset(m->err_flag, 0, 4));
-      return fail(T5H_ERR_INVALID, "token id outside the vocabulary");
-    }
+  if (*(volatile unsigned*)m->err_host) {
+    *(volatile unsigned*)m->err_host = 0;
+    return fail(T5H_ERR_INVALID, "token id outside the vocabulary");
   }
   return T5H_OK;
 }
@@ -728,6 +735,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   }
   bind(m->proj);
   HIP_OK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  if (hipHostMalloc((void**)&m->err_host, 256, hipHostMallocMapped) != hipSuccess)
+    return fail(T5H_ERR_NOMEM, "pinned flag allocation failed");
+  *(volatile unsigned*)m->err_host = 0;
+  HIP_OK(hipHostGetDevicePointer((void**)&m->err_flag, m->err_host, 0));
   for (int k = 0; k < K_COUNT; k++) m->stats[k].name = kKernelNames[k];
   *out = m.release();
   g_err.clear();
