@@ -74,18 +74,24 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const bool live = t < T;
   const int nblk = D >> 5;
   const float* xr = x + (size_t)(live ? t : 0) * D + c8;
-  float4 keep[RN_KEEP][2];
-  float ss = 0.f;
+  // x and gamma of the kept blocks are requested together: one memory round trip
+  float4 keep[RN_KEEP][2], gk[RN_KEEP][2];
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
     const int kb = wave + 4 * j;
-    keep[j][0] = keep[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live && kb < nblk) {
-      keep[j][0] = *reinterpret_cast<const float4*>(xr + kb * 32);
-      keep[j][1] = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
-      ss += sq4(keep[j][0]) + sq4(keep[j][1]);
+    keep[j][0] = keep[j][1] = gk[j][0] = gk[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (kb < nblk) {
+      gk[j][0] = *reinterpret_cast<const float4*>(w + kb * 32 + c8);
+      gk[j][1] = *reinterpret_cast<const float4*>(w + kb * 32 + c8 + 4);
+      if (live) {
+        keep[j][0] = *reinterpret_cast<const float4*>(xr + kb * 32);
+        keep[j][1] = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
+      }
     }
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < RN_KEEP; ++j) ss += sq4(keep[j][0]) + sq4(keep[j][1]);
   for (int kb = wave + 4 * RN_KEEP; live && kb < nblk; kb += 4)
     ss += sq4(*reinterpret_cast<const float4*>(xr + kb * 32)) +
           sq4(*reinterpret_cast<const float4*>(xr + kb * 32 + 4));
@@ -96,9 +102,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const float tot = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
   const float inv = 1.0f / sqrtf(tot / (float)D + eps);
   _Float16* ob = out + (size_t)blockIdx.x * nblk * 512 + lane * 8;
-  auto emit = [&](int kb, float4 a, float4 b) {
-    const float4 ga = *reinterpret_cast<const float4*>(w + kb * 32 + c8);
-    const float4 gb = *reinterpret_cast<const float4*>(w + kb * 32 + c8 + 4);
+  auto emit = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
     h8 o = h8{(_Float16)((a.x * inv) * ga.x), (_Float16)((a.y * inv) * ga.y),
               (_Float16)((a.z * inv) * ga.z), (_Float16)((a.w * inv) * ga.w),
               (_Float16)((b.x * inv) * gb.x), (_Float16)((b.y * inv) * gb.y),
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
     const int kb = wave + 4 * j;
-    if (kb < nblk) emit(kb, keep[j][0], keep[j][1]);
+    if (kb < nblk) emit(kb, keep[j][0], keep[j][1], gk[j][0], gk[j][1]);
   }
   for (int kb = wave + 4 * RN_KEEP; kb < nblk; kb += 4) {
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
@@ -116,7 +120,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       a = *reinterpret_cast<const float4*>(xr + kb * 32);
       b = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
     }
-    emit(kb, a, b);
+    emit(kb, a, b, *reinterpret_cast<const float4*>(w + kb * 32 + c8),
+         *reinterpret_cast<const float4*>(w + kb * 32 + c8 + 4));
   }
 }
 
