@@ -175,17 +175,124 @@ def query_bench(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+PEAK_F32_MFMA_TFLOPS = 157.3  # MI355X dense f32 MFMA
+
+
+def _event_time(torch, fn, reps: int) -> float:
+    """Average seconds per call of `fn` over `reps` back-to-back launches, from HIP events on
+    torch's current stream (the stream the scoring kernels are enqueued on)."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def score_bench(args) -> None:
+    """Query-side scoring (src/lib.rs:734-735): 32 query-token embeddings x N indexed residual
+    embeddings (128-d f32) -> [32, N] scores, one matmul_t per step, all buffers resident in
+    HBM.  HBM-bound: N*512 B of residuals + 32*N*4 B of scores per launch.  Also reports the
+    k-means assignment step (src/lib.rs:233-236): matmul_argmax of `--kmeans-m` sampled rows
+    against `--kmeans-k` centers, f32 MFMA-bound, in the f32 (candle) and bf16-B (fbgemm)
+    numerics."""
+    import torch
+
+    from witchcraft_amd import score
+
+    M, D, N = 32, 128, args.score_n
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn((M, D), device=dev, generator=g)
+    q /= q.norm(dim=1, keepdim=True)
+    res = torch.randn((N, D), device=dev, generator=g) * 0.1
+    out = torch.empty((M, N), device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+
+    def step():
+        score.matmul_t_device(q.data_ptr(), M, res.data_ptr(), N, D, out.data_ptr(), stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    avg_s = _event_time(torch, step, args.steps)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    value = M * N * args.steps / elapsed
+    bytes_per_launch = N * D * 4 + M * D * 4 + M * N * 4
+    achieved = bytes_per_launch / avg_s / 1e9
+    log(f"[bench] score: {args.steps} x matmul_t [{M},{D}]x[{N},{D}]^T: {avg_s * 1e6:.1f} us/launch, "
+        f"{achieved:.0f} GB/s")
+
+    # k-means assignment: compute-bound leg
+    km, kk = args.kmeans_m, args.kmeans_k
+    data = torch.randn((km, D), device=dev, generator=g)
+    cent = torch.randn((kk, D), device=dev, generator=g)
+    asg = torch.empty(km, dtype=torch.int32, device=dev)
+    kmeans = {}
+    for bf in (False, True):
+        def kstep(bf=bf):
+            score.matmul_argmax_device(data.data_ptr(), km, cent.data_ptr(), kk, D, asg.data_ptr(), bf16_b=bf,
+                                       stream=stream)
+        kstep()
+        ks = _event_time(torch, kstep, max(3, args.steps // 4))
+        tf = 2.0 * km * kk * D / ks / 1e12
+        kmeans["bf16_b" if bf else "f32"] = {"avg_launch_us": ks * 1e6, "tflops": tf,
+                                             "mfma_frac": tf / PEAK_F32_MFMA_TFLOPS}
+        log(f"[bench] kmeans assign {'bf16_b' if bf else 'f32'} [{km}x{kk}]: {ks * 1e3:.2f} ms, {tf:.1f} TFLOP/s")
+
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        r = np.random.default_rng(args.seed)
+        ns = 1 << 17
+        qa = r.standard_normal((M, D)).astype(np.float32)
+        rb = r.standard_normal((ns, D)).astype(np.float32)
+        orc.matmul_t(qa, rb, acc64=False)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_budget, 10.0) or reps == 0:
+            orc.matmul_t(qa, rb, acc64=False)
+            reps += 1
+        cpu_s = (time.perf_counter() - t0) / reps
+        base = {"value": M * ns / cpu_s, "unit": "scores/s", "cores": threads, "kind": "port",
+                "sample": f"{reps} x matmul_t [{M},{D}]x[{ns},{D}]^T in the C oracle (scalar loop per "
+                          f"dot product, OpenMP over query rows)"}
+    line = {
+        "metric": "query x residual scores/sec (fast_ops::matmul_t, 32 x N x 128 f32)", "value": value,
+        "unit": "scores/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"score: 32 query tokens x {N} residual embeddings (d=128), f32, resident in HBM",
+                   "M": M, "N": N, "D": D, "parallelism": "single GPU"},
+        "roofline": {"kernel": "matmul_t_kernel (v_mfma_f32_16x16x4_f32, 32-row tile)", "bound": "hbm",
+                     "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+                     "traffic": None, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
+        "kmeans_assign": {"kernel": "matmul_argmax_kernel", "M": km, "N": kk, "D": D, "bound": "mfma",
+                          "peak_tflops": PEAK_F32_MFMA_TFLOPS, **kmeans},
+        "cpu_baseline": base,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + ["score"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--queries", type=int, default=1000, help="cfg3: number of timed queries")
     ap.add_argument("--rotate", type=int, default=8, help="cfg3: model replicas cycled (MALL defeat)")
+    ap.add_argument("--score-n", type=int, default=1 << 20, help="score: residual rows")
+    ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
+    ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 10 times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -207,6 +314,9 @@ def main() -> None:
 
     if args.workload == "cfg3":
         query_bench(args)
+        return
+    if args.workload == "score":
+        score_bench(args)
         return
 
     import torch

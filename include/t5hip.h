@@ -104,6 +104,27 @@ int t5h_embed_ids(t5h_model* model, const uint32_t* ids, int32_t n_tokens, int32
  * src/quantized_t5.rs:44).  blocks/out are HOST buffers. */
 int t5h_q4k_dequant_f32(const void* blocks, size_t nblk, float* out, int hip_device);
 
+/* ---- Query-side scoring, next to the encoder ----
+ * C[M][N] = A[M][D] . B[N][D]^T in f32: fast_ops::matmul_t (src/fast_ops.rs:98-116) and
+ * PackedRight::matmul (:65-95), as used for query x centroid / residual scores
+ * (src/lib.rs:637,735,759,1646).  bf16_b != 0 truncates B to bf16 first, as the fbgemm build
+ * packs it (fbgemm-rs/src/bf16.rs:21-31); A stays f32 and sums are f32.  Any M, N, D >= 0
+ * (M == 0 or N == 0: nothing to do).  Host buffers, synchronous, on HIP device hip_device. */
+int t5h_matmul_t(int32_t hip_device, const float* a, int32_t M, const float* b, int32_t N, int32_t D,
+                 int32_t bf16_b, float* c);
+/* matmul_argmax_batched (src/lib.rs:187-208, k-means assignment at :235,1330):
+ * out[i] = argmax_j A[i] . B[j], the first (smallest) j on ties as candle's argmax (0 when no
+ * score exceeds -inf).  N > 0.  Same buffers and numerics as t5h_matmul_t, no [M][N]
+ * intermediate. */
+int t5h_matmul_argmax(int32_t hip_device, const float* a, int32_t M, const float* b, int32_t N,
+                      int32_t D, int32_t bf16_b, uint32_t* out);
+/* The same on device buffers of the current device, enqueued on `stream` (a hipStream_t;
+ * NULL = the default stream); they return without waiting. */
+int t5h_matmul_t_device(const float* d_a, int32_t M, const float* d_b, int32_t N, int32_t D,
+                        int32_t bf16_b, float* d_c, void* stream);
+int t5h_matmul_argmax_device(const float* d_a, int32_t M, const float* d_b, int32_t N, int32_t D,
+                             int32_t bf16_b, uint32_t* d_out, void* stream);
+
 /* One T5Block (src/quantized_t5.rs:598-627) on packed sequences: x_in/x_out are
  * host [T, d_model] f32. */
 int t5h_layer_forward(t5h_model* model, int32_t layer, const float* x_in,

@@ -64,6 +64,9 @@ def _load() -> C.CDLL:
     lib.orc_rmsnorm.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_float, f32p, C.c_int]
     lib.orc_softmax_rows.argtypes = [f32p, C.c_int, C.c_int]
     lib.orc_linear.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, f32p, C.c_int]
+    lib.orc_matmul_t.argtypes = [f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int, f32p, C.c_int]
+    lib.orc_matmul_argmax.argtypes = [f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int,
+                                      np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS"), C.c_int]
     lib.orc_model_from_gguf.argtypes = [u8p, C.c_size_t, C.POINTER(OrcConfig), C.c_int,
                                         C.c_char_p, C.c_size_t]
     lib.orc_model_from_gguf.restype = C.c_void_p
@@ -158,6 +161,24 @@ def linear(x: np.ndarray, w: np.ndarray, acc64: bool = True) -> np.ndarray:
 
 
 # ---- model ------------------------------------------------------------------------
+
+def matmul_t(a: np.ndarray, b: np.ndarray, bf16_b: bool = False, acc64: bool = True) -> np.ndarray:
+    """C = A . B^T (src/fast_ops.rs:98-116); bf16_b truncates B first (fbgemm build)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    c = np.empty((a.shape[0], b.shape[0]), np.float32)
+    lib().orc_matmul_t(a, a.shape[0], b, b.shape[0], a.shape[1], int(bf16_b), c, int(acc64))
+    return c
+
+
+def matmul_argmax(a: np.ndarray, b: np.ndarray, bf16_b: bool = False, acc64: bool = True) -> np.ndarray:
+    """First argmax_j of A[i] . B[j] per row (src/lib.rs:187-208)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty(a.shape[0], np.uint32)
+    lib().orc_matmul_argmax(a, a.shape[0], b, b.shape[0], a.shape[1], int(bf16_b), out, int(acc64))
+    return out
+
 
 def make_config(cfg: dict) -> OrcConfig:
     return OrcConfig(

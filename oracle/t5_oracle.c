@@ -338,6 +338,60 @@ void orc_linear(const float* x, const float* w, int T, int N, int K, float* y, i
 }
 
 /* ------------------------------------------------------------------------- */
+/* Query-side scoring next to the encoder.                                     */
+/* ------------------------------------------------------------------------- */
+
+/* fast_ops::matmul_t (src/fast_ops.rs:98-116) / PackedRight::matmul (:65-95): C[M,N] =
+ * A[M,D] . B[N,D]^T.  bf16_b: B truncated to bf16 first (the fbgemm build's
+ * PackedMatrixBf16::from_transposed, fbgemm-rs/src/bf16.rs:21-31), A kept f32.  acc64
+ * accumulates each dot product in double (the reference order is unknown; tests use it). */
+void orc_matmul_t(const float* a, int M, const float* b, int N, int D, int bf16_b, float* c, int acc64) {
+#pragma omp parallel for schedule(static)
+  for (int i = 0; i < M; i++) {
+    const float* ar = a + (size_t)i * D;
+    for (int j = 0; j < N; j++) {
+      const float* br = b + (size_t)j * D;
+      if (acc64) {
+        double s = 0.0;
+        for (int k = 0; k < D; k++) s += (double)ar[k] * (double)(bf16_b ? orc_bf16_trunc(br[k]) : br[k]);
+        c[(size_t)i * N + j] = (float)s;
+      } else {
+        float s = 0.f;
+        for (int k = 0; k < D; k++) s += ar[k] * (bf16_b ? orc_bf16_trunc(br[k]) : br[k]);
+        c[(size_t)i * N + j] = s;
+      }
+    }
+  }
+}
+
+/* matmul_argmax_batched (src/lib.rs:187-208): per row of A, the index of the largest
+ * A[i] . B[j]; candle's argmax keeps the first maximum, so ties go to the smallest j. */
+void orc_matmul_argmax(const float* a, int M, const float* b, int N, int D, int bf16_b, uint32_t* out, int acc64) {
+#pragma omp parallel for schedule(static)
+  for (int i = 0; i < M; i++) {
+    const float* ar = a + (size_t)i * D;
+    double best = -INFINITY;
+    uint32_t bi = 0;
+    for (int j = 0; j < N; j++) {
+      const float* br = b + (size_t)j * D;
+      double s = 0.0;
+      if (acc64) {
+        for (int k = 0; k < D; k++) s += (double)ar[k] * (double)(bf16_b ? orc_bf16_trunc(br[k]) : br[k]);
+      } else {
+        float f = 0.f;
+        for (int k = 0; k < D; k++) f += ar[k] * (bf16_b ? orc_bf16_trunc(br[k]) : br[k]);
+        s = f;
+      }
+      if (j == 0 || s > best) {
+        best = s;
+        bi = (uint32_t)j;
+      }
+    }
+    out[i] = bi;
+  }
+}
+
+/* ------------------------------------------------------------------------- */
 /* GGUF reader (format written by tools/quantize-tool/src/main.rs:33-35 via    */
 /* candle gguf_file::write, read by VarBuilder::from_gguf_buffer at            */
 /* src/quantized_t5.rs:740-743).  Independent of the product's reader.         */

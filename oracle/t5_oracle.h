@@ -58,6 +58,12 @@ void orc_softmax_rows(float* s, int rows, int cols);
 /* y[T,N] = x[T,K] . W[N,K]^T  (f32 math; acc64 = accumulate each dot in double) */
 void orc_linear(const float* x, const float* w, int T, int N, int K, float* y, int acc64);
 
+/* ---- query-side scoring ---- */
+/* c[M,N] = a[M,D] . b[N,D]^T (bf16_b: b truncated to bf16 first) */
+void orc_matmul_t(const float* a, int M, const float* b, int N, int D, int bf16_b, float* c, int acc64);
+/* out[i] = first argmax_j a[i] . b[j] */
+void orc_matmul_argmax(const float* a, int M, const float* b, int N, int D, int bf16_b, uint32_t* out, int acc64);
+
 /* ---- GGUF + model ---- */
 orc_model* orc_model_from_gguf(const uint8_t* buf, size_t len, const orc_config* cfg, int variant,
                                char* err, size_t errlen);

@@ -55,6 +55,10 @@ SIGNATURES = {
     "t5h_embed_ids": (C.c_int, [_vp, _u32p, C.c_int32, C.c_int32, C.c_int32, _f32p, _i32p,
                                 C.POINTER(C.c_int32)]),
     "t5h_q4k_dequant_f32": (C.c_int, [_u8p, C.c_size_t, _f32p, C.c_int]),
+    "t5h_matmul_t": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _f32p]),
+    "t5h_matmul_argmax": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _u32p]),
+    "t5h_matmul_t_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, C.c_int32, _vp, _vp]),
+    "t5h_matmul_argmax_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, C.c_int32, _vp, _vp]),
     "t5h_layer_forward": (C.c_int, [_vp, C.c_int32, _f32p, _i32p, C.c_int32, _f32p]),
     "t5h_ffn_block": (C.c_int, [_vp, C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32]),
     "t5h_set_profiling": (C.c_int, [_vp, C.c_int32]),
@@ -72,6 +76,14 @@ def load() -> C.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
                           "(make -C witchcraft_amd/csrc)")
+    # torch ships its own libamdhip64.so.7 under the same soname as /opt/rocm's, and a process
+    # holds one of them: whichever loads first serves both.  torch's CUDA init fails on a
+    # runtime other than its own ("No HIP GPUs are available"), so when torch is installed
+    # its copy is loaded first and this library binds to it.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(LIB_PATH))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

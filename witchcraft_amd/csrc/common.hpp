@@ -95,6 +95,11 @@ hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, 
                           hipStream_t s);
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s);
+// Query-side scoring: C = A . B^T (f32) and its per-row argmax (k_score.hip).
+hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int N, int D, bool bf16_b,
+                           hipStream_t s);
+hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, int M, int N, int D, bool bf16_b,
+                                hipStream_t s);
 hipError_t launch_window_sum(const float* win_out, const int* src_rows, int n_tokens, int max_windows,
                              int P, float* sum, float* norm, float* normalized, hipStream_t s);
 }  // namespace t5k

@@ -1,0 +1,275 @@
+// k_score.hip -- query-side scoring next to the encoder: C = A . B^T in f32 and its per-row
+// argmax (k-means assignment).
+//
+// Reference: fast_ops::matmul_t (src/fast_ops.rs:98-116) and PackedRight::matmul
+// (:65-95), used for query x centroid / residual scores (src/lib.rs:637,735,759,1646), and
+// matmul_argmax_batched (src/lib.rs:187-208, called at :235,1330).  The default build
+// multiplies f32 x f32 (candle); the fbgemm build first truncates B to bf16
+// (PackedMatrixBf16, fbgemm-rs/src/bf16.rs:21-31) and accumulates in f32 -- bf16_b selects it.
+//
+// f32 MFMA (v_mfma_f32_16x16x4_f32): products are exact f32 as on the CPU.  A lane holds 4
+// consecutive K values of one row (one float4 load from global) and feeds them to 4
+// consecutive MFMAs, each of which sums its K-lane group g = lane / 16 over k = 16 kb + 4 g + j;
+// A and B use the same assignment, so every product a[k] b[k] is summed once.
+//   * matmul_t: wave tile = 16 MB rows x 64 columns, MB = ceil(M / 16) up to 4, so query-sized
+//     M (32 query tokens against many residuals, HBM-bound on B) pads to 16 rows at most.
+//     Workgroup = 4 waves side by side along N (or along M when N <= 64).
+//   * argmax:   workgroup = 4 waves on 64 rows, looping over N in 256-column chunks; the
+//     running (max, index) per row lives in registers, the 4 waves' results meet in LDS.
+//     Ties resolve to the smallest column index (candle's argmax keeps the first maximum).
+#include "common.hpp"
+
+namespace {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ldg4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+__device__ __forceinline__ float4 trunc_bf16(float4 v) {
+  auto t = [](float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x) & 0xffff0000u;
+    return __builtin_bit_cast(float, u);
+  };
+  return make_float4(t(v.x), t(v.y), t(v.z), t(v.w));
+}
+
+// p[0..3] of one row (zero if !ok).  VEC: rows are 16-byte aligned (D % 4 == 0 and aligned
+// bases), so one float4 load; otherwise 4 scalar loads.
+template <bool VEC>
+__device__ __forceinline__ float4 ld4(const float* p, bool ok) {
+  if (VEC) return ok ? ldg4(p) : make_float4(0.f, 0.f, 0.f, 0.f);
+  return ok ? make_float4(p[0], p[1], p[2], p[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// p[j] for j < n (zero past it, or everywhere if !ok): the last, partial K block.
+__device__ __forceinline__ float4 ld4_tail(const float* p, int n, bool ok) {
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) v[j] = (ok && j < n) ? p[j] : 0.f;
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <int MB>
+__device__ __forceinline__ void mfma_4x4(const float4 (&a)[4], const float4 (&b)[4], f4v (&acc)[4][4]) {
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+      // B as the MFMA A operand: lane ends with 4 consecutive columns of one row
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[nb].x, a[mb].x, acc[mb][nb], 0, 0, 0);
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[nb].y, a[mb].y, acc[mb][nb], 0, 0, 0);
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[nb].z, a[mb].z, acc[mb][nb], 0, 0, 0);
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[nb].w, a[mb].w, acc[mb][nb], 0, 0, 0);
+    }
+}
+
+// acc[mb][nb] += A[rows 16mb..] . B[cols 16nb..]^T over all of K for a 16 MB x 64 wave tile;
+// rows / columns outside the matrices and K past D read as zero.  Full 16-wide K blocks run
+// unguarded; the last partial block (D % 16 != 0) masks per element.
+template <int MB, bool BF16B, bool VEC>
+__device__ __forceinline__ void wave_tile(const float* __restrict__ A, const float* __restrict__ B, int M,
+                                           int N, int D, int r0, int c0, int lane, f4v (&acc)[4][4]) {
+  const int lr = lane & 15, lg = lane >> 4;
+  const float* ar[4];
+  const float* br[4];
+  bool av[4], bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = r0 + 16 * i + lr, c = c0 + 16 * i + lr;
+    av[i] = r < M;
+    bv[i] = c < N;
+    ar[i] = A + (size_t)(av[i] ? r : 0) * D + 4 * lg;
+    br[i] = B + (size_t)(bv[i] ? c : 0) * D + 4 * lg;
+  }
+  const int dfull = D & ~15;
+  for (int kb = 0; kb < dfull; kb += 16) {
+    float4 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      a[i] = i < MB ? ld4<VEC>(ar[i] + kb, av[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      b[i] = ld4<VEC>(br[i] + kb, bv[i]);
+      if (BF16B) b[i] = trunc_bf16(b[i]);
+    }
+    mfma_4x4<MB>(a, b, acc);
+  }
+  if (dfull < D) {
+    // this lane's 4 values are k = dfull + 4 lg + j, of which the first D - dfull - 4 lg exist
+    const int n = D - dfull - 4 * lg;
+    float4 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      a[i] = i < MB ? ld4_tail(ar[i] + dfull, n, av[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      b[i] = ld4_tail(br[i] + dfull, n, bv[i]);
+      if (BF16B) b[i] = trunc_bf16(b[i]);
+    }
+    mfma_4x4<MB>(a, b, acc);
+  }
+}
+
+// With B as the MFMA A operand (16 columns) and A as the B operand (16 rows), lane l holds
+// C[row 16mb + (l % 16)][cols 16nb + 4(l / 16) + 0..3].  wn = waves of the workgroup along N
+// (4, or 1 when N <= 64, then the 4 waves stack along M).
+template <int MB, bool BF16B, bool VEC>
+__global__ __launch_bounds__(256) void matmul_t_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int D, int wn,
+                                                       int tiles_n) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wm = 4 / wn;
+  // 1-D grid, column tiles fastest: workgroups in flight share rows of A and walk B in order
+  const int bm = blockIdx.x / tiles_n, bn = blockIdx.x - bm * tiles_n;
+  const int r0 = (bm * wm + wave / wn) * 16 * MB, c0 = (bn * wn + wave % wn) * 64;
+  if (r0 >= M || c0 >= N) return;  // wave-uniform; no workgroup barrier follows
+  f4v acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+  wave_tile<MB, BF16B, VEC>(A, B, M, N, D, r0, c0, lane, acc);
+  const int lr = lane & 15, lg = lane >> 4;
+  const bool vec_out = (N & 3) == 0 && VEC;
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+    const int r = r0 + 16 * mb + lr;
+    if (r >= M) continue;
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+      const int c = c0 + 16 * nb + 4 * lg;
+      float* out = C + (size_t)r * N + c;
+      if (vec_out && c + 3 < N) {
+        *reinterpret_cast<float4*>(out) = make_float4(acc[mb][nb][0], acc[mb][nb][1], acc[mb][nb][2], acc[mb][nb][3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (c + i < N) out[i] = acc[mb][nb][i];
+      }
+    }
+  }
+}
+
+// (v, i) beats (w, j) if v > w, or v == w and i < j (first maximum wins).
+__device__ __forceinline__ void amax_merge(float& v, int& i, float w, int j) {
+  if (w > v || (w == v && j < i)) {
+    v = w;
+    i = j;
+  }
+}
+
+template <bool BF16B, bool VEC>
+__global__ __launch_bounds__(256) void matmul_argmax_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                            uint32_t* __restrict__ out, int M, int N, int D) {
+  __shared__ float sv[4][64];
+  __shared__ int si[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.x * 64;
+  // running maximum of row 16mb + lr (identical in the 4 lanes of that row); starting from
+  // (-inf, 0) keeps the result in range when no score exceeds -inf (NaN or -inf rows give 0)
+  float bv[4];
+  int bi[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++) {
+    bv[mb] = -INFINITY;
+    bi[mb] = 0;
+  }
+  for (int n0 = 0; n0 < N; n0 += 256) {
+    const int c0 = n0 + wave * 64;
+    if (c0 >= N) break;  // wave-uniform
+    f4v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+    wave_tile<4, BF16B, VEC>(A, B, M, N, D, r0, c0, lane, acc);
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+      float v = -INFINITY;
+      int ix = 0x7fffffff;
+#pragma unroll
+      for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int c = c0 + 16 * nb + 4 * lg + i;
+          if (c < N) amax_merge(v, ix, acc[mb][nb][i], c);
+        }
+      // combine the 4 lanes (lg = 0..3) holding this row: lanes l ^ 16, l ^ 32
+#pragma unroll
+      for (int o = 16; o <= 32; o <<= 1) {
+        const float w = __shfl_xor(v, o);
+        const int j = __shfl_xor(ix, o);
+        amax_merge(v, ix, w, j);
+      }
+      amax_merge(bv[mb], bi[mb], v, ix);
+    }
+  }
+  if (lg == 0)
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+      sv[wave][16 * mb + lr] = bv[mb];
+      si[wave][16 * mb + lr] = bi[mb];
+    }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int t = threadIdx.x, r = r0 + t;
+    float v = sv[0][t];
+    int ix = si[0][t];
+    for (int w = 1; w < 4; w++) amax_merge(v, ix, sv[w][t], si[w][t]);
+    if (r < M) out[r] = (uint32_t)ix;
+  }
+}
+
+}  // namespace
+
+namespace t5k {
+namespace {
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+}  // namespace
+
+hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int N, int D, bool bf16_b,
+                           hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  if (D < 0) return hipErrorInvalidValue;
+  const int mb = M >= 64 ? 4 : (M + 15) / 16;
+  const int wn = N <= 64 ? 1 : 4, wm = 4 / wn;
+  const long tiles_n = (N + 64L * wn - 1) / (64L * wn), tiles_m = (M + 16L * mb * wm - 1) / (16L * mb * wm);
+  if (tiles_n * tiles_m > 0x7fffffffL) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(tiles_n * tiles_m));
+  const bool vec = D % 4 == 0 && aligned16(A) && aligned16(B) && aligned16(C);
+#define T5K_MMT(MBV, BF, VEC) \
+  hipLaunchKernelGGL((matmul_t_kernel<MBV, BF, VEC>), grid, dim3(256), 0, s, A, B, C, M, N, D, wn, (int)tiles_n)
+#define T5K_MMT_MB(BF, VEC)      \
+  switch (mb) {                  \
+    case 1: T5K_MMT(1, BF, VEC); break; \
+    case 2: T5K_MMT(2, BF, VEC); break; \
+    case 3: T5K_MMT(3, BF, VEC); break; \
+    default: T5K_MMT(4, BF, VEC); break; \
+  }
+  if (bf16_b) {
+    if (vec) { T5K_MMT_MB(true, true) } else { T5K_MMT_MB(true, false) }
+  } else {
+    if (vec) { T5K_MMT_MB(false, true) } else { T5K_MMT_MB(false, false) }
+  }
+#undef T5K_MMT_MB
+#undef T5K_MMT
+  return hipGetLastError();
+}
+
+hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, int M, int N, int D, bool bf16_b,
+                                hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  if (N <= 0 || D < 0) return hipErrorInvalidValue;
+  const dim3 grid((M + 63) / 64);
+  const bool vec = D % 4 == 0 && aligned16(A) && aligned16(B);
+  if (bf16_b) {
+    if (vec)
+      hipLaunchKernelGGL((matmul_argmax_kernel<true, true>), grid, dim3(256), 0, s, A, B, out, M, N, D);
+    else
+      hipLaunchKernelGGL((matmul_argmax_kernel<true, false>), grid, dim3(256), 0, s, A, B, out, M, N, D);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((matmul_argmax_kernel<false, true>), grid, dim3(256), 0, s, A, B, out, M, N, D);
+    else
+      hipLaunchKernelGGL((matmul_argmax_kernel<false, false>), grid, dim3(256), 0, s, A, B, out, M, N, D);
+  }
+  return hipGetLastError();
+}
+}  // namespace t5k

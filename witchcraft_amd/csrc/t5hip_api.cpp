@@ -748,6 +748,38 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
 }  // namespace
 
 // =================================================================================
+namespace {
+// argmax needs N > 0 (an argmax over no columns is undefined); matmul_t allows N == 0.
+int check_score_args(const void* a, int32_t M, const void* b, int32_t N, int32_t D, const void* out, bool argmax) {
+  if (M < 0 || N < 0 || D < 0) return fail(T5H_ERR_INVALID, "scoring needs M, N, D >= 0");
+  if (argmax && N == 0 && M > 0) return fail(T5H_ERR_INVALID, "argmax over N == 0 columns");
+  if (M > 0 && N > 0 && (!a || !b || !out)) return fail(T5H_ERR_INVALID, "NULL buffer");
+  return T5H_OK;
+}
+
+// Host-buffer scoring call: upload A and B, run `launch` (which writes out_bytes at d_out),
+// download.  All device memory is released on every path.
+template <typename Launch>
+int score_host(int32_t hip_device, const float* a, int32_t M, const float* b, int32_t N, int32_t D, void* out,
+               size_t out_bytes, Launch launch) {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(T5H_ERR_NODEVICE, "no HIP device");
+  HIP_OK(hipSetDevice(hip_device < 0 ? 0 : hip_device));
+  // sub-buffers on 256-byte boundaries so the kernels' 16-byte vector loads stay available
+  const size_t a_bytes = ((size_t)M * D * 4 + 255) & ~(size_t)255, b_bytes = ((size_t)N * D * 4 + 255) & ~(size_t)255;
+  char* d = nullptr;
+  if (hipMalloc((void**)&d, a_bytes + b_bytes + out_bytes) != hipSuccess)
+    return fail(T5H_ERR_NOMEM, "scoring buffers");
+  std::unique_ptr<void, void (*)(void*)> g(d, [](void* p) { (void)hipFree(p); });
+  HIP_OK(hipMemcpy(d, a, (size_t)M * D * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(d + a_bytes, b, (size_t)N * D * 4, hipMemcpyHostToDevice));
+  HIP_OK(launch((const float*)d, (const float*)(d + a_bytes), (void*)(d + a_bytes + b_bytes)));
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(out, d + a_bytes + b_bytes, out_bytes, hipMemcpyDeviceToHost));
+  return T5H_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* t5h_last_error(void) { return g_err.c_str(); }
@@ -890,6 +922,42 @@ int t5h_q4k_dequant_f32(const void* blocks, size_t nblk, float* out, int hip_dev
   HIP_OK(t5k::launch_q4k_dequant(d_in, nblk, d_out, nullptr));
   HIP_OK(hipDeviceSynchronize());
   HIP_OK(hipMemcpy(out, d_out, nblk * QK_K * 4, hipMemcpyDeviceToHost));
+  return T5H_OK;
+}
+
+int t5h_matmul_t(int32_t hip_device, const float* a, int32_t M, const float* b, int32_t N, int32_t D, int32_t bf16_b,
+                 float* c) {
+  int rc;
+  if ((rc = check_score_args(a, M, b, N, D, c, false))) return rc;
+  if (M == 0 || N == 0) return T5H_OK;
+  return score_host(hip_device, a, M, b, N, D, c, (size_t)M * N * 4, [&](const float* da, const float* db, void* dc) {
+    return t5k::launch_matmul_t(da, db, (float*)dc, M, N, D, bf16_b != 0, nullptr);
+  });
+}
+
+int t5h_matmul_argmax(int32_t hip_device, const float* a, int32_t M, const float* b, int32_t N, int32_t D,
+                      int32_t bf16_b, uint32_t* out) {
+  int rc;
+  if ((rc = check_score_args(a, M, b, N, D, out, true))) return rc;
+  if (M == 0) return T5H_OK;
+  return score_host(hip_device, a, M, b, N, D, out, (size_t)M * 4, [&](const float* da, const float* db, void* dout) {
+    return t5k::launch_matmul_argmax(da, db, (uint32_t*)dout, M, N, D, bf16_b != 0, nullptr);
+  });
+}
+
+int t5h_matmul_t_device(const float* d_a, int32_t M, const float* d_b, int32_t N, int32_t D, int32_t bf16_b,
+                        float* d_c, void* stream) {
+  int rc;
+  if ((rc = check_score_args(d_a, M, d_b, N, D, d_c, false))) return rc;
+  HIP_OK(t5k::launch_matmul_t(d_a, d_b, d_c, M, N, D, bf16_b != 0, (hipStream_t)stream));
+  return T5H_OK;
+}
+
+int t5h_matmul_argmax_device(const float* d_a, int32_t M, const float* d_b, int32_t N, int32_t D, int32_t bf16_b,
+                             uint32_t* d_out, void* stream) {
+  int rc;
+  if ((rc = check_score_args(d_a, M, d_b, N, D, d_out, true))) return rc;
+  HIP_OK(t5k::launch_matmul_argmax(d_a, d_b, d_out, M, N, D, bf16_b != 0, (hipStream_t)stream));
   return T5H_OK;
 }
 
