@@ -19,9 +19,16 @@
 //     Ties resolve to the smallest column index (candle's argmax keeps the first maximum).
 #include "common.hpp"
 
+#include <algorithm>
+#include <atomic>
+
 namespace {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Word 3 of a raw (stride 0) buffer descriptor on gfx9-family GPUs: 32-bit data format, so
+// an access beyond num_records returns zero (loads) or is dropped (stores).
+constexpr int kBufDword3 = 0x00020000;
 
 __device__ __forceinline__ float4 ldg4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
@@ -146,6 +153,118 @@ __global__ __launch_bounds__(256) void matmul_t_kernel(const float* __restrict__
   }
 }
 
+// Query-sized A (M <= 16 MB <= 32) against a long B of 128-d rows, N % 4 == 0
+// (src/lib.rs:734-735): a stream over B.  Persistent waves; wave w takes 32-column tiles
+// w, w + W, w + 2W, ... (W = all waves of the grid, so the waves in flight cover one
+// contiguous stretch of B).  A sits in LDS for the whole run, and the next tile's B loads
+// are issued before the current tile's MFMAs and stores, so HBM streams while the f32
+// MFMAs run.
+template <int MB, bool BF16B>
+__global__ __launch_bounds__(256, 2) void matmul_t_stream_kernel(const float* __restrict__ A,
+                                                                 const float* __restrict__ B,
+                                                                 float* __restrict__ C, int M, int N) {
+  constexpr int D = 128, KB = D / 16, AS = D / 4 + 1;  // A row stride in LDS: 33 float4
+  __shared__ float4 As[16 * MB * AS];
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  // wave index made visibly uniform, so tile bases and descriptors live in scalar registers
+  const int w0 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = gridDim.x * 4;
+  const int ntiles = (N + 31) / 32, nfull = N / 32, tail_bytes = (N % 32) * D * 4;
+  // A (16 MB rows, rows past M repeat row M - 1) into LDS once; no barrier after this one
+  for (int e = threadIdx.x; e < 16 * MB * (D / 4); e += 256) {
+    const int r = e / (D / 4), q = e - r * (D / 4);
+    As[r * AS + q] = ldg4(A + (size_t)min(r, M - 1) * D + 4 * q);
+  }
+  __syncthreads();
+  // B tile t through a buffer descriptor whose range ends at column N: columns past N (the
+  // last tile's tail, and the prefetch past the last tile) read as zero without touching
+  // memory.  Lane offsets are loop-invariant, so no address registers live across the loop.
+  const int voff[2] = {(lr * D + 4 * lg) * 4, ((16 + lr) * D + 4 * lg) * 4};
+  auto load = [&](int t, float4 (&b)[KB][2]) {
+    // (selected on the tile index rather than clamped: a clamp becomes a vector med3, whose
+    // result register the allocator may take from a load still in flight)
+    const int bytes = t < nfull ? 32 * D * 4 : (t == nfull ? tail_bytes : 0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(B + (size_t)t * 32 * D), (short)0, bytes, kBufDword3);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int kb = 0; kb < KB; kb++) {
+        const f4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[nb] + 64 * kb, 0, 0);
+        b[kb][nb] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+  };
+  auto compute = [&](const float4 (&b)[KB][2], f4v (&acc)[MB][2]) {
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) acc[i][nb] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const float4 bb = BF16B ? trunc_bf16(b[kb][nb]) : b[kb][nb];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+          const float4 a = As[(16 * i + lr) * AS + 4 * kb + lg];
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bb.x, a.x, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bb.y, a.y, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bb.z, a.z, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bb.w, a.w, acc[i][nb], 0, 0, 0);
+        }
+      }
+  };
+  // lane holds C[16 i + lr][32 t + 16 nb + 4 lg + 0..3]; N % 4 == 0, so a lane's 4 columns
+  // are all inside or all outside [0, N)
+  // (stores through a descriptor based at column 32 t; row offsets r N 4 < 2^31 is a launch
+  // condition)
+  int soff[MB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) soff[i] = ((16 * i + lr) * N + 4 * lg) * 4;
+  auto store = [&](int t, const f4v (&acc)[MB][2]) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(C + (size_t)t * 32), (short)0, 0x7fffffff, kBufDword3);
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+      const bool row_ok = 16 * i + lr < M;
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+        if (row_ok && 32 * t + 16 * nb + 4 * lg < N)
+          __builtin_amdgcn_raw_buffer_store_b128(acc[i][nb], rs, soff[i] + 64 * nb, 0, 0);
+    }
+  };
+  // Per tile: issue the next tile's loads, then the previous tile's stores, then this tile's
+  // MFMAs.  Loads and stores share one in-order counter, so stores issued after the next
+  // loads never hold up the wait for this tile's data.  Two tiles per trip let the B and
+  // accumulator buffers alternate without copies; every bound is wave-uniform.  (The
+  // scheduling barriers keep that issue order.)
+  float4 b0[KB][2], b1[KB][2];
+  f4v acc0[MB][2], acc1[MB][2];
+  int t = w0, t1 = -1;  // t1: tile whose results wait in acc1
+  load(t, b0);
+  while (t < ntiles) {
+    load(t + nw, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t1 >= 0) store(t1, acc1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b0, acc0);
+    const int t0 = t;
+    t += nw;
+    t1 = -1;
+    if (t >= ntiles) {
+      store(t0, acc0);
+      break;
+    }
+    load(t + nw, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    store(t0, acc0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b1, acc1);
+    t1 = t;
+    t += nw;
+  }
+  if (t1 >= 0) store(t1, acc1);
+}
+
 // (v, i) beats (w, j) if v > w, or v == w and i < j (first maximum wins).
 __device__ __forceinline__ void amax_merge(float& v, int& i, float w, int j) {
   if (w > v || (w == v && j < i)) {
@@ -222,6 +341,19 @@ __global__ __launch_bounds__(256) void matmul_argmax_kernel(const float* __restr
 namespace t5k {
 namespace {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// compute units of the current device (cached per device; 256 if the query fails)
+int num_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 }  // namespace
 
 hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int N, int D, bool bf16_b,
@@ -234,6 +366,18 @@ hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int 
   if (tiles_n * tiles_m > 0x7fffffffL) return hipErrorInvalidValue;
   const dim3 grid((unsigned)(tiles_n * tiles_m));
   const bool vec = D % 4 == 0 && aligned16(A) && aligned16(B) && aligned16(C);
+  if (vec && D == 128 && M <= 32 && N >= 4096 && N % 4 == 0 && 32L * N * 4 < (1L << 31)) {
+    // query x residuals: persistent streaming kernel, 2 workgroups per CU
+    const int wgs = (int)std::min<long>(2L * num_cus(), (N + 127) / 128);
+    if (mb == 1) {
+      if (bf16_b) hipLaunchKernelGGL((matmul_t_stream_kernel<1, true>), dim3(wgs), dim3(256), 0, s, A, B, C, M, N);
+      else hipLaunchKernelGGL((matmul_t_stream_kernel<1, false>), dim3(wgs), dim3(256), 0, s, A, B, C, M, N);
+    } else {
+      if (bf16_b) hipLaunchKernelGGL((matmul_t_stream_kernel<2, true>), dim3(wgs), dim3(256), 0, s, A, B, C, M, N);
+      else hipLaunchKernelGGL((matmul_t_stream_kernel<2, false>), dim3(wgs), dim3(256), 0, s, A, B, C, M, N);
+    }
+    return hipGetLastError();
+  }
 #define T5K_MMT(MBV, BF, VEC) \
   hipLaunchKernelGGL((matmul_t_kernel<MBV, BF, VEC>), grid, dim3(256), 0, s, A, B, C, M, N, D, wn, (int)tiles_n)
 #define T5K_MMT_MB(BF, VEC)      \
