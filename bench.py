@@ -228,6 +228,12 @@ def score_bench(args) -> None:
     log(f"[bench] score: {args.steps} x matmul_t [{M},{D}]x[{N},{D}]^T: {avg_s * 1e6:.1f} us/launch, "
         f"{achieved:.0f} GB/s")
 
+    traffic = None
+    tfile = ROOT / "profiles" / "score_traffic.json"
+    if N == 1 << 20 and tfile.exists():
+        t = json.loads(tfile.read_text())["bytes_per_dispatch"]["matmul_t_stream_kernel"]
+        traffic = t["fetch"] + t["write"]
+
     # k-means assignment: compute-bound leg
     km, kk = args.kmeans_m, args.kmeans_k
     data = torch.randn((km, D), device=dev, generator=g)
@@ -269,9 +275,9 @@ def score_bench(args) -> None:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"score: 32 query tokens x {N} residual embeddings (d=128), f32, resident in HBM",
                    "M": M, "N": N, "D": D, "parallelism": "single GPU"},
-        "roofline": {"kernel": "matmul_t_kernel (v_mfma_f32_16x16x4_f32, 32-row tile)", "bound": "hbm",
+        "roofline": {"kernel": "matmul_t_stream_kernel (persistent, v_mfma_f32_16x16x4_f32)", "bound": "hbm",
                      "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
-                     "traffic": None, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
+                     "traffic": traffic, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
         "kmeans_assign": {"kernel": "matmul_argmax_kernel", "M": km, "N": kk, "D": D, "bound": "mfma",
                           "peak_tflops": PEAK_F32_MFMA_TFLOPS, **kmeans},
         "cpu_baseline": base,

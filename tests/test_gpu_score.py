@@ -47,6 +47,12 @@ SHAPES = [
     (3, 4096, 96),     # D % 16 != 0 (tail block), D % 4 == 0 (vector loads)
     (7, 5, 13),        # unaligned rows: scalar loads
     (1, 70, 1),
+    # the persistent streaming kernel (M <= 32, D = 128, N >= 4096, N % 4 == 0)
+    (32, 65536, 128),  # query tokens x residuals
+    (17, 4100, 128),   # 2 row blocks; last 32-column tile holds 4 columns
+    (16, 8192, 128),   # one row block
+    (1, 4124, 128),    # single query row; last tile holds 28 columns
+    (32, 4098, 128),   # N % 4 != 0: the tiled kernel instead
 ]
 
 
@@ -61,6 +67,7 @@ def test_matmul_t_vs_oracle(score, M, N, D, bf16_b):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     bound = _bound(a, b, bf16_b)
     assert np.all(err <= bound), f"max err/bound {(err / bound).max():.3f}"
+    assert np.all(np.isfinite(got))
 
 
 def test_matmul_t_d_zero_is_zero(score):
@@ -112,6 +119,18 @@ def test_matmul_argmax_vs_oracle(score, M, N, D, bf16_b):
     assert n_clear >= 0.9 * M
 
 
+@pytest.mark.parametrize("bf16_b", [False, True])
+def test_matmul_argmax_many_rows_vs_oracle(score, bf16_b):
+    # M >= 256 x CUs routes to the register-A / LDS-B kernel; 300 columns = 4 full 64-column
+    # chunks + 44, M = 512 x 128 + 37 leaves a partial last workgroup
+    M, N, D = 65573, 300, 128
+    print(f"argmax rows M={M} N={N} bf16_b={bf16_b}", flush=True)
+    a, b = _data(M, N, D, seed=77)
+    got = score.matmul_argmax(a, b, bf16_b=bf16_b)
+    assert np.all(got < N)
+    assert _check_argmax(a, b, got, bf16_b) >= 0.99 * M
+
+
 def test_matmul_argmax_exact_ties_first_index(score):
     r = np.random.default_rng(12)
     base = r.standard_normal((40, 128)).astype(np.float32)
@@ -131,12 +150,17 @@ def test_matmul_argmax_exact_ties_first_index(score):
     assert clear.sum() > 100
     # all scores equal: index 0
     np.testing.assert_array_equal(score.matmul_argmax(np.zeros((70, 128), np.float32), b), np.zeros(70, np.uint32))
+    # the same through the many-rows kernel
+    big = np.tile(a, (450, 1))
+    got_big = score.matmul_argmax(big, b)
+    np.testing.assert_array_equal(got_big[:150][clear], first[clear])
+    np.testing.assert_array_equal(got_big.reshape(450, 150), np.tile(got_big[:150], (450, 1)))
 
 
 def test_packed_right_device_path(score):
     import torch
 
-    a, b = _data(32, 2048, 128, seed=9)
+    a, b = _data(32, 8192, 128, seed=9)  # the streaming kernel's shape
     pr = score.PackedRight(b)
     np.testing.assert_array_equal(pr.matmul(a), score.matmul_t(a, b))
     np.testing.assert_array_equal(pr.argmax(a), score.matmul_argmax(a, b))
@@ -149,9 +173,9 @@ def test_packed_right_device_path(score):
     s = torch.cuda.Stream()
     da = torch.from_numpy(a).cuda()
     db = torch.from_numpy(b).cuda()
-    dc = torch.empty((32, 2048), device="cuda", dtype=torch.float32)
+    dc = torch.empty((32, 8192), device="cuda", dtype=torch.float32)
     torch.cuda.synchronize()
-    score.matmul_t_device(da.data_ptr(), 32, db.data_ptr(), 2048, 128, dc.data_ptr(), stream=s.cuda_stream)
+    score.matmul_t_device(da.data_ptr(), 32, db.data_ptr(), 8192, 128, dc.data_ptr(), stream=s.cuda_stream)
     s.synchronize()
     np.testing.assert_array_equal(dc.cpu().numpy(), score.matmul_t(a, b))
 

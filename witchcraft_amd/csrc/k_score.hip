@@ -336,6 +336,104 @@ __global__ __launch_bounds__(256) void matmul_argmax_kernel(const float* __restr
   }
 }
 
+// k-means assignment (src/lib.rs:233-236, 1330) at D = 128 and large M: MFMA-bound.  Each
+// wave owns 32 rows of A, held in registers for the whole run (16 float4 per lane); the 4
+// waves of a workgroup share each 64-column chunk of B through LDS (double-buffered: the
+// next chunk's global loads are issued before this chunk's MFMAs, one barrier per chunk).
+// Global traffic per MFMA is a quarter of the per-wave tile above, which was bound by
+// L2 -> CU bandwidth.  Per row: running (max, first index), as in matmul_argmax_kernel.
+template <bool BF16B>
+__global__ __launch_bounds__(256, 2) void matmul_argmax_rows_kernel(const float* __restrict__ A,
+                                                                    const float* __restrict__ B,
+                                                                    uint32_t* __restrict__ out, int M, int N) {
+  constexpr int D = 128, KB = D / 16, BS = D / 4 + 1, RB = 2;  // LDS row stride: 33 float4
+  __shared__ float4 Bs[2][64 * BS];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.x * (64 * RB) + wave * (16 * RB);
+  // A fragments: row r0 + 16 mb + lr, K slice 16 kb + 4 lg; rows past M repeat row M - 1
+  // (their results are not stored)
+  float4 a[KB][4];
+#pragma unroll
+  for (int mb = 0; mb < RB; mb++) {
+    const float* p = A + (size_t)min(r0 + 16 * mb + lr, M - 1) * D + 4 * lg;
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) a[kb][mb] = ldg4(p + 16 * kb);
+  }
+  // chunk loader: thread tid moves float4 q = tid + 256 j (j < 8) of the 64 x 32 float4 chunk;
+  // columns past N repeat column N - 1 (masked out of the argmax)
+  float4 st[8];
+  auto gload = [&](int n0) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int q = tid + 256 * j, c = q >> 5, k4 = q & 31;
+      st[j] = ldg4(B + (size_t)min(n0 + c, N - 1) * D + 4 * k4);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int q = tid + 256 * j, c = q >> 5, k4 = q & 31;
+      Bs[buf][c * BS + k4] = BF16B ? trunc_bf16(st[j]) : st[j];
+    }
+  };
+  float bv[RB];
+  int bi[RB];
+#pragma unroll
+  for (int mb = 0; mb < RB; mb++) {
+    bv[mb] = -INFINITY;
+    bi[mb] = 0;
+  }
+  const int nchunks = (N + 63) / 64;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int ch = 0; ch < nchunks; ch++) {
+    const int buf = ch & 1, n0 = ch * 64;
+    if (ch + 1 < nchunks) gload(n0 + 64);
+    f4v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      float4 b[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; nb++) b[nb] = Bs[buf][(16 * nb + lr) * BS + 4 * kb + lg];
+      mfma_4x4<RB>(a[kb], b, acc);
+    }
+#pragma unroll
+    for (int mb = 0; mb < RB; mb++) {
+      float v = -INFINITY;
+      int ix = 0x7fffffff;
+#pragma unroll
+      for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int c = n0 + 16 * nb + 4 * lg + i;
+          if (c < N) amax_merge(v, ix, acc[mb][nb][i], c);
+        }
+#pragma unroll
+      for (int o = 16; o <= 32; o <<= 1) {
+        const float w = __shfl_xor(v, o);
+        const int j = __shfl_xor(ix, o);
+        amax_merge(v, ix, w, j);
+      }
+      amax_merge(bv[mb], bi[mb], v, ix);
+    }
+    if (ch + 1 < nchunks) {
+      lstore(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  if (lg == 0)
+#pragma unroll
+    for (int mb = 0; mb < RB; mb++) {
+      const int r = r0 + 16 * mb + lr;
+      if (r < M) out[r] = (uint32_t)bi[mb];
+    }
+}
+
 }  // namespace
 
 namespace t5k {
@@ -401,8 +499,17 @@ hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, i
                                 hipStream_t s) {
   if (M <= 0) return hipSuccess;
   if (N <= 0 || D < 0) return hipErrorInvalidValue;
-  const dim3 grid((M + 63) / 64);
   const bool vec = D % 4 == 0 && aligned16(A) && aligned16(B);
+  if (vec && D == 128 && M >= 256L * num_cus()) {
+    // enough rows for two 128-row workgroups per CU: the register-A / LDS-B kernel
+    const dim3 g((M + 127) / 128);
+    if (bf16_b)
+      hipLaunchKernelGGL((matmul_argmax_rows_kernel<true>), g, dim3(256), 0, s, A, B, out, M, N);
+    else
+      hipLaunchKernelGGL((matmul_argmax_rows_kernel<false>), g, dim3(256), 0, s, A, B, out, M, N);
+    return hipGetLastError();
+  }
+  const dim3 grid((M + 63) / 64);
   if (bf16_b) {
     if (vec)
       hipLaunchKernelGGL((matmul_argmax_kernel<true, true>), grid, dim3(256), 0, s, A, B, out, M, N, D);
