@@ -234,6 +234,44 @@ def score_bench(args) -> None:
         t = json.loads(tfile.read_text())["bytes_per_dispatch"]["matmul_t_stream_kernel"]
         traffic = t["fetch"] + t["write"]
 
+    # The same scores straight from 4-bit residual codes (src/lib.rs:676-680,734-735 without the
+    # f32 residual matrix): N*64 B of codes + 32*N*4 B of scores per launch.
+    from witchcraft_amd import codec
+    codes = torch.randint(0, 256, (N, D // 2), dtype=torch.uint8, device=dev, generator=g)
+
+    def qstep():
+        codec.matmul_t_q4_device(q.data_ptr(), M, codes.data_ptr(), N, D, out.data_ptr(), stream=stream)
+
+    qstep()
+    qs = _event_time(torch, qstep, args.steps)
+    q_bytes = N * D // 2 + M * D * 4 + M * N * 4
+    q_tf = 2.0 * M * N * D / qs / 1e12
+    q4 = {"kernel": "matmul_t_q4_stream_kernel (codes -> LDS table -> v_mfma_f32_16x16x4_f32)",
+          "avg_launch_us": qs * 1e6, "bytes_per_launch": q_bytes, "gbs": q_bytes / qs / 1e9,
+          "hbm_frac": q_bytes / qs / 1e9 / PEAK_HBM_GBS, "tflops": q_tf, "mfma_frac": q_tf / PEAK_F32_MFMA_TFLOPS,
+          "scores_per_s": M * N / qs, "speedup_vs_f32_residuals": avg_s / qs}
+    log(f"[bench] score from q4 codes: {qs * 1e6:.1f} us/launch ({avg_s / qs:.2f}x the f32 residuals), "
+        f"{q_bytes / qs / 1e9:.0f} GB/s, {q_tf:.1f} TFLOP/s f32")
+
+    # Index build: residual codes of N embeddings against their assigned centres
+    # (src/lib.rs:1375-1376): N*512 B in, N*64 B out (centres stay in L2).
+    kc = 1 << 14
+    cent_e = torch.randn((kc, D), device=dev, generator=g)
+    asg_e = torch.randint(0, kc, (N,), dtype=torch.int32, device=dev, generator=g)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def estep():
+        codec.residual_encode_device(res.data_ptr(), N, cent_e.data_ptr(), kc, asg_e.data_ptr(), D,
+                                     codes.data_ptr(), bad.data_ptr(), stream=stream)
+
+    estep()
+    es = _event_time(torch, estep, args.steps)
+    e_bytes = N * D * 4 + N * 4 + N * D // 2
+    enc = {"kernel": "residual_encode_kernel (threshold ladder)", "avg_launch_us": es * 1e6,
+           "rows_per_s": N / es, "bytes_per_launch": e_bytes, "gbs": e_bytes / es / 1e9,
+           "hbm_frac": e_bytes / es / 1e9 / PEAK_HBM_GBS}
+    log(f"[bench] residual encode [{N}x{D}]: {es * 1e6:.1f} us, {e_bytes / es / 1e9:.0f} GB/s")
+
     # k-means assignment: compute-bound leg
     km, kk = args.kmeans_m, args.kmeans_k
     data = torch.randn((km, D), device=dev, generator=g)
@@ -268,6 +306,15 @@ def score_bench(args) -> None:
         base = {"value": M * ns / cpu_s, "unit": "scores/s", "cores": threads, "kind": "port",
                 "sample": f"{reps} x matmul_t [{M},{D}]x[{ns},{D}]^T in the C oracle (scalar loop per "
                           f"dot product, OpenMP over query rows)"}
+        ce = r.standard_normal((kc, D)).astype(np.float32)
+        ca = r.integers(0, kc, ns).astype(np.uint32)
+        orc.residual_encode(rb, ce, ca)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0 or reps == 0:
+            orc.residual_encode(rb, ce, ca)
+            reps += 1
+        enc["cpu_rows_per_s"] = ns * reps / (time.perf_counter() - t0)
+        enc["cpu_sample"] = f"{reps} x residual_encode of {ns} rows in the C oracle, OpenMP over rows, {threads} threads"
     line = {
         "metric": "query x residual scores/sec (fast_ops::matmul_t, 32 x N x 128 f32)", "value": value,
         "unit": "scores/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -278,6 +325,8 @@ def score_bench(args) -> None:
         "roofline": {"kernel": "matmul_t_stream_kernel (persistent, v_mfma_f32_16x16x4_f32)", "bound": "hbm",
                      "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
+        "q4_scoring": q4,
+        "residual_encode": enc,
         "kmeans_assign": {"kernel": "matmul_argmax_kernel", "M": km, "N": kk, "D": D, "bound": "mfma",
                           "peak_tflops": PEAK_F32_MFMA_TFLOPS, **kmeans},
         "cpu_baseline": base,

@@ -125,6 +125,37 @@ int t5h_matmul_t_device(const float* d_a, int32_t M, const float* d_b, int32_t N
 int t5h_matmul_argmax_device(const float* d_a, int32_t M, const float* d_b, int32_t N, int32_t D,
                              int32_t bf16_b, uint32_t* d_out, void* stream);
 
+/* ---- The residual codec of the index, next to the encoder (src/packops.rs) ----
+ * A residual (token embedding minus its k-means centre) is stored as 4-bit codes,
+ * compand().quantize(4).to_q4_bytes() (packops.rs:136-142,156-162,440-462): two codes per
+ * byte, value 2j of a row in the high nibble of byte j.  Search decodes them through
+ * make_q4_dequant_table (packops.rs:14-25) in from_companded_q4_bytes (:491-513). */
+
+/* make_q4_dequant_table (src/packops.rs:14-25): the f32 value of each 4-bit code. */
+int t5h_q4_dequant_table(float table[16]);
+/* The 15 decision thresholds of compand().quantize(4): code(x) = number of thresholds <= x
+ * (NaN -> 0).  No counterpart in the reference; exposed so callers and tests can check the
+ * exact encoding the GPU applies. */
+int t5h_q4_compand_thresholds(float thresholds[15]);
+/* Index build (src/lib.rs:1375-1376): codes[i] = to_q4_bytes(compand(emb[i] -
+ * centers[assign[i]]).quantize(4)); emb[N][D], centers[K][D], codes[N][D/2], D % 8 == 0.
+ * Host buffers, synchronous.  An assignment >= K is an error. */
+int t5h_residual_encode(int32_t hip_device, const float* emb, int32_t N, const float* centers, int32_t K,
+                        const uint32_t* assign, int32_t D, uint8_t* codes);
+/* Device-buffer form on `stream`; rows whose assignment is >= K get zero bytes and set *d_bad
+ * (a device word the caller zeroes). */
+int t5h_residual_encode_device(const float* d_emb, int32_t N, const float* d_centers, int32_t K,
+                               const uint32_t* d_assign, int32_t D, uint8_t* d_codes, uint32_t* d_bad, void* stream);
+/* from_companded_q4_bytes (src/packops.rs:491-513): codes[N][D/2] -> out[N][D] f32, D even. */
+int t5h_residual_decode(int32_t hip_device, const uint8_t* codes, int32_t N, int32_t D, float* out);
+int t5h_residual_decode_device(const uint8_t* d_codes, int32_t N, int32_t D, float* d_out, void* stream);
+/* Search-time residual scores without materialising the residuals (src/lib.rs:676-680,734-735):
+ * C[M][N] = A[M][D] . from_companded_q4_bytes(codes)[N][D]^T in f32, D % 4 == 0. */
+int t5h_matmul_t_q4(int32_t hip_device, const float* a, int32_t M, const uint8_t* codes, int32_t N, int32_t D,
+                    float* c);
+int t5h_matmul_t_q4_device(const float* d_a, int32_t M, const uint8_t* d_codes, int32_t N, int32_t D, float* d_c,
+                           void* stream);
+
 /* One T5Block (src/quantized_t5.rs:598-627) on packed sequences: x_in/x_out are
  * host [T, d_model] f32. */
 int t5h_layer_forward(t5h_model* model, int32_t layer, const float* x_in,

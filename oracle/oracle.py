@@ -78,6 +78,22 @@ def _load() -> C.CDLL:
     lib.orc_final.argtypes = [C.c_void_p, f32p, C.c_int, f32p, C.c_int]
     lib.orc_position_bias.argtypes = [C.c_void_p, C.c_int, f32p]
     lib.orc_embed_ids.argtypes = [C.c_void_p, u32p, C.c_int, C.c_int, C.c_int, f32p, i32p, C.c_int]
+    # embedding codecs (codec_oracle.c)
+    lib.orc_compand_q4.argtypes = [C.c_float]
+    lib.orc_compand_q4.restype = C.c_uint8
+    lib.orc_q4_dequant_table.argtypes = [f32p]
+    lib.orc_residual_encode.argtypes = [f32p, f32p, u32p, C.c_int, C.c_int, u8p]
+    lib.orc_residual_decode.argtypes = [u8p, C.c_int, C.c_int, f32p, f32p]
+    lib.orc_ladder_mismatches.argtypes = [f32p, C.POINTER(C.c_uint32)]
+    lib.orc_ladder_mismatches.restype = C.c_uint64
+    lib.orc_haar_forward.argtypes = [f32p, C.c_int]
+    lib.orc_haar_inverse.argtypes = [f32p, C.c_int]
+    lib.orc_scale_histogram.argtypes = [u32p, C.c_int, C.c_int,
+                                        np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")]
+    lib.orc_embeddings_to_packed.argtypes = [f32p, C.c_int, C.c_int, u8p, C.c_size_t]
+    lib.orc_embeddings_to_packed.restype = C.c_long
+    lib.orc_embeddings_from_packed.argtypes = [u8p, C.c_size_t, C.c_int, f32p, C.c_size_t]
+    lib.orc_embeddings_from_packed.restype = C.c_long
     return lib
 
 
@@ -269,3 +285,93 @@ class OracleModel:
         if nk < 0:
             raise ValueError("all token embeddings below minimum norm threshold")
         return out[:nk], kept[:nk]
+
+
+# ---- embedding codecs (codec_oracle.c) -------------------------------------------------
+
+def compand_q4(x: float) -> int:
+    """compand().quantize(4) of one f32 value (packops.rs:136-162)."""
+    return int(lib().orc_compand_q4(float(np.float32(x))))
+
+
+def q4_dequant_table() -> np.ndarray:
+    """make_q4_dequant_table (packops.rs:14-25)."""
+    t = np.empty(16, np.float32)
+    lib().orc_q4_dequant_table(t)
+    return t
+
+
+def residual_encode(emb: np.ndarray, centers: np.ndarray, assign: np.ndarray) -> np.ndarray:
+    """residual.compand().quantize(4).to_q4_bytes() per row (src/lib.rs:1375-1376)."""
+    emb = np.ascontiguousarray(emb, np.float32)
+    N, D = emb.shape
+    out = np.empty((N, D // 2), np.uint8)
+    lib().orc_residual_encode(emb, np.ascontiguousarray(centers, np.float32),
+                              np.ascontiguousarray(assign, np.uint32), N, D, out)
+    return out
+
+
+def residual_decode(codes: np.ndarray, D: int, table: np.ndarray | None = None) -> np.ndarray:
+    """from_companded_q4_bytes (packops.rs:491-513)."""
+    codes = np.ascontiguousarray(codes, np.uint8).reshape(-1)
+    N = codes.size * 2 // D
+    out = np.empty((N, D), np.float32)
+    lib().orc_residual_decode(codes, N, D, q4_dequant_table() if table is None else
+                              np.ascontiguousarray(table, np.float32), out)
+    return out
+
+
+def ladder_mismatches(thresholds: np.ndarray) -> tuple[int, int]:
+    """Exhaustive check of a 15-step threshold ladder against compand_q4 (all 2^32 f32)."""
+    bad = C.c_uint32(0)
+    n = lib().orc_ladder_mismatches(np.ascontiguousarray(thresholds, np.float32), C.byref(bad))
+    return int(n), int(bad.value)
+
+
+def haar_forward(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    lib().orc_haar_forward(y, y.size)
+    return y
+
+
+def haar_inverse(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    lib().orc_haar_inverse(y, y.size)
+    return y
+
+
+def scale_histogram(counts: np.ndarray, log2_scale: int = 12) -> np.ndarray:
+    c = np.ascontiguousarray(counts, np.uint32)
+    out = np.empty(c.size, np.uint16)
+    if lib().orc_scale_histogram(c, c.size, log2_scale, out):
+        raise ValueError("scale_histogram: the reference asserts on this input")
+    return out
+
+
+def embeddings_to_packed(x: np.ndarray) -> bytes:
+    """embeddings_to_packed (packops.rs:172-301)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    cap = 4 + (rows // 1024 + 1) * (cols + 2 + 4 * 65536 + 2 + 2 * 1024 * cols + 16)
+    cap = min(cap, 4 + (rows // 1024 + 1) * (cols + 6 + 4 * 4096) + 2 * rows * cols + 64 * (rows // 1024 + 1))
+    out = np.empty(cap, np.uint8)
+    n = lib().orc_embeddings_to_packed(x, rows, cols, out, cap)
+    if n == -2:
+        out = np.empty(4 + (rows // 1024 + 1) * (cols + 6 + 4 * 65536 + 16) + 2 * rows * cols, np.uint8)
+        n = lib().orc_embeddings_to_packed(x, rows, cols, out, out.size)
+    if n < 0:
+        raise ValueError("embeddings_to_packed failed (the reference errors or panics on this input)")
+    return out[:n].tobytes()
+
+
+def embeddings_from_packed(buf: bytes, cols: int = 128) -> np.ndarray:
+    """embeddings_from_packed (packops.rs:303-438): rows L2-normalised."""
+    b = np.frombuffer(buf, np.uint8).copy()
+    if b.size < 4:
+        raise ValueError("buffer too short")
+    rows = int(np.frombuffer(buf[:4], np.uint32)[0])
+    out = np.empty((rows, cols), np.float32)
+    n = lib().orc_embeddings_from_packed(b, b.size, cols, out.reshape(-1) if rows else np.empty(1, np.float32), rows)
+    if n < 0:
+        raise ValueError("malformed packed embeddings")
+    return out

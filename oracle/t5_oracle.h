@@ -93,6 +93,19 @@ int orc_embed_ids(const orc_model* m, const uint32_t* ids, int n_tokens, int max
 
 int orc_model_dims(const orc_model* m, orc_config* cfg);
 
+/* ---- embedding codecs (codec_oracle.c: packops.rs, haarops.rs, rans64.rs) ---- */
+uint8_t orc_compand_q4(float v);          /* compand().quantize(4) of one value */
+void orc_q4_dequant_table(float table[16]); /* make_q4_dequant_table */
+void orc_residual_encode(const float* emb, const float* centers, const uint32_t* assign, int N, int D,
+                         uint8_t* out);
+void orc_residual_decode(const uint8_t* bytes, int N, int D, const float table[16], float* out);
+uint64_t orc_ladder_mismatches(const float t[15], uint32_t* first_bad);
+void orc_haar_forward(float* x, int n);
+void orc_haar_inverse(float* x, int n);
+int orc_scale_histogram(const uint32_t* counts, int m, int log2_scale, uint16_t* freq);
+long orc_embeddings_to_packed(const float* x, int rows, int cols, uint8_t* out, size_t cap);
+long orc_embeddings_from_packed(const uint8_t* buf, size_t len, int cols, float* out, size_t cap_rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,14 @@ SIGNATURES = {
     "t5h_matmul_argmax": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _u32p]),
     "t5h_matmul_t_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, C.c_int32, _vp, _vp]),
     "t5h_matmul_argmax_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, C.c_int32, _vp, _vp]),
+    "t5h_q4_dequant_table": (C.c_int, [_f32p]),
+    "t5h_q4_compand_thresholds": (C.c_int, [_f32p]),
+    "t5h_residual_encode": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, _u32p, C.c_int32, _u8p]),
+    "t5h_residual_encode_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, _vp, C.c_int32, _vp, _vp, _vp]),
+    "t5h_residual_decode": (C.c_int, [C.c_int32, _u8p, C.c_int32, C.c_int32, _f32p]),
+    "t5h_residual_decode_device": (C.c_int, [_vp, C.c_int32, C.c_int32, _vp, _vp]),
+    "t5h_matmul_t_q4": (C.c_int, [C.c_int32, _f32p, C.c_int32, _u8p, C.c_int32, C.c_int32, _f32p]),
+    "t5h_matmul_t_q4_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
     "t5h_layer_forward": (C.c_int, [_vp, C.c_int32, _f32p, _i32p, C.c_int32, _f32p]),
     "t5h_ffn_block": (C.c_int, [_vp, C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32]),
     "t5h_set_profiling": (C.c_int, [_vp, C.c_int32]),

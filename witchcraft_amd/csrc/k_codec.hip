@@ -1,0 +1,298 @@
+// k_codec.hip -- the residual codec of the XTR-WARP index next to the encoder, and scoring
+// straight from its 4-bit codes.
+//
+// Reference (src/packops.rs, src/lib.rs):
+//   * index build: residual = embedding - assigned centre, compand() (mu-law, :136-142),
+//     quantize(4) (:156-162), to_q4_bytes (:440-462) -- src/lib.rs:1375-1376;
+//   * search: from_companded_q4_bytes (:491-513) through make_q4_dequant_table (:14-25), then
+//     matmul_t(query, residuals) -- src/lib.rs:626,676-680,734-735.
+//
+// Encoding never evaluates the mu-law on the GPU: compand().quantize(4) is a non-decreasing
+// step function of the f32 input, so the host finds its 15 thresholds once (bisection over
+// the ordered f32 values, evaluating the reference's own op sequence) and a code is the count
+// of thresholds at or below the value -- exact by construction, NaN -> 0 as the clamp gives.
+// Decoding is the reference's 16-entry table lookup.
+//
+// Scoring reads the codes, not decoded f32: a 128-d residual row is 64 bytes instead of 512,
+// so the stream over residuals moves 8x fewer input bytes.  Products run on
+// v_mfma_f32_16x16x4_f32 (exact f32 products, as the f32 path).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace t5k {
+struct Q4Table {
+  float v[16];
+};
+struct Q4Ladder {
+  float t[15];
+};
+}  // namespace t5k
+
+namespace {
+
+using t5k::Q4Ladder;
+using t5k::Q4Table;
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+constexpr int kBufDword3 = 0x00020000;  // raw buffer descriptor word 3: 32-bit data, OOB -> 0
+
+__device__ __forceinline__ uint32_t q4_code(float r, const Q4Ladder& lad) {
+  uint32_t q = 0;
+#pragma unroll
+  for (int j = 0; j < 15; j++) q += r >= lad.t[j] ? 1u : 0u;
+  return q;
+}
+
+// One thread per 8 values (4 code bytes) of a row; D % 8 == 0.  Rows whose assignment is out
+// of range get zero bytes and raise *bad.
+__global__ __launch_bounds__(256) void residual_encode_kernel(const float* __restrict__ emb,
+                                                              const float* __restrict__ centers,
+                                                              const uint32_t* __restrict__ assign, int N, int D,
+                                                              int K, Q4Ladder lad, uint8_t* __restrict__ out,
+                                                              unsigned* __restrict__ bad) {
+  const int groups = D / 8;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)N * groups) return;
+  const int row = (int)(idx / groups), g = (int)(idx % groups);
+  const uint32_t a = assign[row];
+  uint32_t word = 0;
+  if (a < (uint32_t)K) {
+    const float* e = emb + (size_t)row * D + 8 * g;
+    const float* c = centers + (size_t)a * D + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      const uint32_t hi = q4_code(e[j] - c[j], lad), lo = q4_code(e[j + 1] - c[j + 1], lad);
+      word |= ((hi << 4) | lo) << (4 * j);  // byte j/2: value j in the high nibble
+    }
+  } else if (g == 0) {
+    atomicOr(bad, 1u);
+  }
+  *reinterpret_cast<uint32_t*>(out + (size_t)row * (D / 2) + 4 * g) = word;
+}
+
+// from_companded_q4_bytes: one thread per 4 code bytes -> 8 floats.
+__global__ __launch_bounds__(256) void residual_decode_kernel(const uint8_t* __restrict__ codes, size_t nbytes,
+                                                              Q4Table tab, float* __restrict__ out) {
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) lut[threadIdx.x] = tab.v[threadIdx.x];
+  __syncthreads();
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= nbytes) return;
+  float v[8];
+  const int n = nbytes - i < 4 ? (int)(nbytes - i) : 4;
+  for (int b = 0; b < n; b++) {
+    const uint32_t x = codes[i + b];
+    v[2 * b] = lut[x >> 4];
+    v[2 * b + 1] = lut[x & 15];
+  }
+  for (int j = 0; j < 2 * n; j++) out[2 * i + j] = v[j];
+}
+
+// Query-sized A (M <= 32 rows, D = 128) against N coded residual rows: the stream of
+// matmul_t_stream_kernel (k_score.hip) over 64-byte code rows.  Wave w takes 32-row tiles
+// w, w + W, ...; lane (lr, lg) owns rows lr and 16 + lr of a tile and their values
+// k = 32 lg .. 32 lg + 31 (16 contiguous code bytes), which it feeds to the MFMAs as
+// k = 32 lg + 4 s + j in step s; A is read from LDS with the same assignment, so every product
+// appears once.  C[m][n] for rows n >= N is computed from zero bytes and never stored.
+template <int MB>
+__global__ __launch_bounds__(256, 2) void matmul_t_q4_stream_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ codes, Q4Table tab,
+                                                                    float* __restrict__ C, int M, int N) {
+  constexpr int D = 128, AS = D / 4 + 1;
+  __shared__ float4 As[16 * MB * AS];
+  __shared__ float lut[16];
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int w0 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = gridDim.x * 4;
+  const int ntiles = (N + 31) / 32, nfull = N / 32, tail_bytes = (N % 32) * (D / 2);
+  for (int e = threadIdx.x; e < 16 * MB * (D / 4); e += 256) {
+    const int r = e / (D / 4), q = e - r * (D / 4);
+    As[r * AS + q] = *reinterpret_cast<const float4*>(A + (size_t)min(r, M - 1) * D + 4 * q);
+  }
+  if (threadIdx.x < 16) lut[threadIdx.x] = tab.v[threadIdx.x];
+  __syncthreads();
+  const int voff[2] = {lr * (D / 2) + 16 * lg, (16 + lr) * (D / 2) + 16 * lg};
+  auto load = [&](int t, uint4 (&b)[2]) {
+    const int bytes = t < nfull ? 32 * (D / 2) : (t == nfull ? tail_bytes : 0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(codes + (size_t)t * 32 * (D / 2)), (short)0, bytes, kBufDword3);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const f4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[nb], 0, 0);
+      b[nb] = __builtin_bit_cast(uint4, v);
+    }
+  };
+  auto compute = [&](const uint4 (&b)[2], f4v (&acc)[MB][2]) {
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) acc[i][nb] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const uint32_t w = (s < 2 ? b[nb].x : s < 4 ? b[nb].y : s < 6 ? b[nb].z : b[nb].w) >> (16 * (s & 1));
+        // bytes 2s (values 4s, 4s+1) and 2s+1 (values 4s+2, 4s+3): high nibble first
+        const float v0 = lut[(w >> 4) & 15], v1 = lut[w & 15], v2 = lut[(w >> 12) & 15], v3 = lut[(w >> 8) & 15];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+          const float4 a = As[(16 * i + lr) * AS + 8 * lg + s];
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0, a.x, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1, a.y, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v2, a.z, acc[i][nb], 0, 0, 0);
+          acc[i][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v3, a.w, acc[i][nb], 0, 0, 0);
+        }
+      }
+  };
+  int soff[MB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) soff[i] = ((16 * i + lr) * N + 4 * lg) * 4;
+  auto store = [&](int t, const f4v (&acc)[MB][2]) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(C + (size_t)t * 32), (short)0, 0x7fffffff, kBufDword3);
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+      const bool row_ok = 16 * i + lr < M;
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+        if (row_ok && 32 * t + 16 * nb + 4 * lg < N)
+          __builtin_amdgcn_raw_buffer_store_b128(acc[i][nb], rs, soff[i] + 64 * nb, 0, 0);
+    }
+  };
+  // Same issue order as matmul_t_stream_kernel: next tile's loads, previous tile's stores,
+  // this tile's MFMAs, two tiles per trip.
+  uint4 b0[2], b1[2];
+  f4v acc0[MB][2], acc1[MB][2];
+  int t = w0, t1 = -1;
+  load(t, b0);
+  while (t < ntiles) {
+    load(t + nw, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t1 >= 0) store(t1, acc1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b0, acc0);
+    const int t0 = t;
+    t += nw;
+    t1 = -1;
+    if (t >= ntiles) {
+      store(t0, acc0);
+      break;
+    }
+    load(t + nw, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    store(t0, acc0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b1, acc1);
+    t1 = t;
+    t += nw;
+  }
+  if (t1 >= 0) store(t1, acc1);
+}
+
+// Any M, D % 4 == 0: 64 x 64 workgroup tiles (4 waves of 16 rows x 64 columns), each lane
+// owning k = kb + 4 lg .. +3 of one A row and one code row per 16-block of K.
+__global__ __launch_bounds__(256) void matmul_t_q4_kernel(const float* __restrict__ A,
+                                                          const uint8_t* __restrict__ codes, Q4Table tab,
+                                                          float* __restrict__ C, int M, int N, int D) {
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) lut[threadIdx.x] = tab.v[threadIdx.x];
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.y * 64 + wave * 16, c0 = blockIdx.x * 64;
+  if (r0 >= M) return;  // no barrier follows
+  const int r = r0 + lr;
+  const bool rok = r < M;
+  const float* ar = A + (size_t)(rok ? r : 0) * D;
+  const uint8_t* br[4];
+  bool bok[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++) {
+    const int c = c0 + 16 * nb + lr;
+    bok[nb] = c < N;
+    br[nb] = codes + (size_t)(bok[nb] ? c : 0) * (D / 2);
+  }
+  f4v acc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++) acc[nb] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < D; kb += 16) {
+    const int k = kb + 4 * lg;
+    const bool kok = k < D;  // D % 4 == 0: a lane's 4 values are all in or all out
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (rok && kok) a = make_float4(ar[k], ar[k + 1], ar[k + 2], ar[k + 3]);  // any alignment
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bok[nb] && kok) {
+        const uint32_t x0 = br[nb][k / 2], x1 = br[nb][k / 2 + 1];
+        v[0] = lut[x0 >> 4];
+        v[1] = lut[x0 & 15];
+        v[2] = lut[x1 >> 4];
+        v[3] = lut[x1 & 15];
+      }
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[0], a.x, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[1], a.y, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[2], a.z, acc[nb], 0, 0, 0);
+      acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[3], a.w, acc[nb], 0, 0, 0);
+    }
+  }
+  // lane holds C[r0 + lr][c0 + 16 nb + 4 lg + 0..3]
+  if (!rok) return;
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++) {
+    const int c = c0 + 16 * nb + 4 * lg;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (c + i < N) C[(size_t)r * N + c + i] = acc[nb][i];
+  }
+}
+
+int num_cus_codec() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+}  // namespace
+
+namespace t5k {
+
+hipError_t launch_residual_encode(const float* emb, const float* centers, const uint32_t* assign, int N, int D,
+                                  int K, const Q4Ladder& lad, uint8_t* out, unsigned* bad, hipStream_t s) {
+  if (N <= 0) return hipSuccess;
+  const size_t threads = (size_t)N * (D / 8);
+  hipLaunchKernelGGL(residual_encode_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, emb, centers,
+                     assign, N, D, K, lad, out, bad);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_decode(const uint8_t* codes, size_t nbytes, const Q4Table& tab, float* out,
+                                  hipStream_t s) {
+  if (nbytes == 0) return hipSuccess;
+  const size_t threads = (nbytes + 3) / 4;
+  hipLaunchKernelGGL(residual_decode_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, codes, nbytes,
+                     tab, out);
+  return hipGetLastError();
+}
+
+// C[M][N] = A[M][D] . decode(codes[N][D/2])^T.  D % 4 == 0.
+hipError_t launch_matmul_t_q4(const float* A, const uint8_t* codes, const Q4Table& tab, float* C, int M, int N,
+                              int D, hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  const bool aligned = ((uintptr_t)A & 15) == 0 && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)C & 15) == 0;
+  if (D == 128 && M <= 32 && N % 4 == 0 && N >= 4096 && aligned && (size_t)N * 4 * 32 < 0x7fffffffu) {
+    const int wgs = std::min(2 * num_cus_codec(), (N + 127) / 128);
+    if (M <= 16) hipLaunchKernelGGL((matmul_t_q4_stream_kernel<1>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+    else hipLaunchKernelGGL((matmul_t_q4_stream_kernel<2>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+    return hipGetLastError();
+  }
+  const dim3 grid((N + 63) / 64, (M + 63) / 64);
+  hipLaunchKernelGGL(matmul_t_q4_kernel, grid, dim3(256), 0, s, A, codes, tab, C, M, N, D);
+  return hipGetLastError();
+}
+
+}  // namespace t5k

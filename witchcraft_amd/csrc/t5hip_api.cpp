@@ -27,6 +27,14 @@ int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+}  // namespace
+
+namespace t5h_detail {
+// The same thread-local message for the entry points defined in other files (codec.cpp).
+int fail(int code, const std::string& msg) { return ::fail(code, msg); }
+}  // namespace t5h_detail
+
+namespace {
 
 #define HIP_OK(expr)                                                                   \
   do {                                                                                 \
