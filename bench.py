@@ -334,12 +334,69 @@ def score_bench(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def codec_bench(args) -> None:
+    """Chunk-embedding codec after the encoder (src/lib.rs:1091 embeddings_to_packed per chunk,
+    decoded at :712,1178,1296): a batch of `--codec-docs` matrices of L ~ U[64, 512] unit
+    128-d rows (the cfg4 document lengths), packed and unpacked in one GPU call each.  The
+    value is the encoder side's throughput in embedding rows/s over the GPU time of the call's
+    kernels (inputs already in HBM; the call's own PCIe copies are reported separately)."""
+    from witchcraft_amd import codec
+
+    r = np.random.default_rng(args.seed)
+    lens = r.integers(64, 513, args.codec_docs)
+    mats = []
+    for L in lens:
+        base = r.normal(0, 1, 128)
+        x = base + np.cumsum(r.normal(0, 0.15, (L, 128)), axis=0) + r.normal(0, 0.3, (L, 128))
+        mats.append((x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32))
+    rows = int(lens.sum())
+    packed, _ = codec.embeddings_to_packed_batch(mats, timing=True)  # warm-up
+    enc_ms, dec_ms, wall = [], [], []
+    for _ in range(max(3, args.steps // 4)):
+        t = time.perf_counter()
+        packed, ms = codec.embeddings_to_packed_batch(mats, timing=True)
+        wall.append(time.perf_counter() - t)
+        enc_ms.append(ms)
+        _, ms = codec.embeddings_from_packed_batch(packed, 128, timing=True)
+        dec_ms.append(ms)
+    enc = sorted(enc_ms)[len(enc_ms) // 2] * 1e-3
+    dec = sorted(dec_ms)[len(dec_ms) // 2] * 1e-3
+    nbytes = sum(len(b) for b in packed)
+    log(f"[bench] codec: {len(mats)} chunks, {rows} rows: pack {enc * 1e3:.2f} ms GPU "
+        f"({rows / enc:.3g} rows/s), unpack {dec * 1e3:.2f} ms GPU, {8 * nbytes / (rows * 128):.2f} bits/value")
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        sample = mats[: max(1, len(mats) // 8)]
+        srows = sum(m.shape[0] for m in sample)
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min(args.cpu_budget, 10.0) or reps == 0:
+            for m in sample:
+                orc.embeddings_to_packed(m)
+            reps += 1
+        cpu = (time.perf_counter() - t0) / reps
+        base = {"value": srows / cpu, "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"{reps} x embeddings_to_packed of {len(sample)} chunks ({srows} rows) in the C oracle, "
+                          f"one chunk after another on one thread as src/lib.rs:1091 does"}
+    line = {
+        "metric": "packed chunk-embedding encode rows/sec (embeddings_to_packed, 128-d)", "value": rows / enc,
+        "unit": "rows/s", "n_gpus": 1, "steps": len(enc_ms), "warmup": 1, "ms_per_step": enc * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"codec: {len(mats)} chunks of L ~ U[64,512] unit 128-d rows ({rows} rows)",
+                   "parallelism": "single GPU"},
+        "decode_rows_per_s": rows / dec, "decode_ms": dec * 1e3, "bits_per_value": 8 * nbytes / (rows * 128),
+        "encode_call_wall_ms": sorted(wall)[len(wall) // 2] * 1e3,
+        "cpu_baseline": base,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + ["score"])
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + ["score", "codec"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -348,6 +405,7 @@ def main() -> None:
     ap.add_argument("--score-n", type=int, default=1 << 20, help="score: residual rows")
     ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
     ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
+    ap.add_argument("--codec-docs", type=int, default=256, help="codec: chunks per batch")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 10 times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -372,6 +430,9 @@ def main() -> None:
         return
     if args.workload == "score":
         score_bench(args)
+        return
+    if args.workload == "codec":
+        codec_bench(args)
         return
 
     import torch

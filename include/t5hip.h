@@ -156,6 +156,30 @@ int t5h_matmul_t_q4(int32_t hip_device, const float* a, int32_t M, const uint8_t
 int t5h_matmul_t_q4_device(const float* d_a, int32_t M, const uint8_t* d_codes, int32_t N, int32_t D, float* d_c,
                            void* stream);
 
+/* ---- Packed chunk embeddings (src/packops.rs:172-438) ----
+ * embeddings_to_packed / embeddings_from_packed over a batch of B matrices of `cols` columns
+ * (1..255; Witchcraft stores each chunk's [L', 128] token embeddings this way, src/lib.rs:1091,
+ * decoded at :712,1178,1296).  Per matrix: u32 rows, then per window of <= 1024 rows the column
+ * permutation, the rANS frequency table and one rANS64 stream (2-D Haar coefficients, columns
+ * sorted by sum, quantised to round(29 x / max|x|<1)).  Bytes equal the reference's.
+ * Host buffers, synchronous; gpu_ms (may be NULL) receives the device time of the call's
+ * kernels.  Errors: T5H_ERR_INVALID where the reference panics or asserts (NaN column sum,
+ * > 4096 distinct symbols, stream overflow) or buffers are too small; T5H_ERR_FORMAT for a
+ * malformed packed buffer (truncated, leftover bytes, corrupt stream, column index >= cols). */
+
+/* x: the matrices' rows back to back, [row_offsets[B]][cols] f32; row_offsets[B+1] with
+ * row_offsets[0] = 0.  out (out_cap bytes) receives the packed matrices back to back;
+ * out_offsets[B+1] their byte offsets (out_offsets[B] = total, also set when out_cap is too
+ * small, so a caller can size the buffer and call again). */
+int t5h_embeddings_to_packed(int32_t hip_device, const float* x, const int32_t* row_offsets, int32_t B,
+                             int32_t cols, uint8_t* out, size_t out_cap, size_t* out_offsets, double* gpu_ms);
+/* buf: B packed matrices back to back, buf_offsets[B+1] their byte offsets.  out receives
+ * the decoded rows (each L2-normalised, as the reference returns them) back to back,
+ * out_cap_rows rows of room; row_offsets[B+1] the row offset of each matrix. */
+int t5h_embeddings_from_packed(int32_t hip_device, const uint8_t* buf, const size_t* buf_offsets, int32_t B,
+                               int32_t cols, float* out, size_t out_cap_rows, int32_t* row_offsets,
+                               double* gpu_ms);
+
 /* One T5Block (src/quantized_t5.rs:598-627) on packed sequences: x_in/x_out are
  * host [T, d_model] f32. */
 int t5h_layer_forward(t5h_model* model, int32_t layer, const float* x_in,

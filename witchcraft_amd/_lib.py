@@ -67,6 +67,12 @@ SIGNATURES = {
     "t5h_residual_decode_device": (C.c_int, [_vp, C.c_int32, C.c_int32, _vp, _vp]),
     "t5h_matmul_t_q4": (C.c_int, [C.c_int32, _f32p, C.c_int32, _u8p, C.c_int32, C.c_int32, _f32p]),
     "t5h_matmul_t_q4_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, _vp, _vp]),
+    "t5h_embeddings_to_packed": (C.c_int, [C.c_int32, _f32p, _i32p, C.c_int32, C.c_int32, _u8p, C.c_size_t,
+                                           np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"),
+                                           C.POINTER(C.c_double)]),
+    "t5h_embeddings_from_packed": (C.c_int, [C.c_int32, _u8p, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"),
+                                             C.c_int32, C.c_int32, _f32p, C.c_size_t, _i32p,
+                                             C.POINTER(C.c_double)]),
     "t5h_layer_forward": (C.c_int, [_vp, C.c_int32, _f32p, _i32p, C.c_int32, _f32p]),
     "t5h_ffn_block": (C.c_int, [_vp, C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32]),
     "t5h_set_profiling": (C.c_int, [_vp, C.c_int32]),

@@ -12,6 +12,8 @@ Everything runs in libt5hip.so; there is no CPU fallback.  Shape errors raise Va
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 
 from ._lib import check, lib
@@ -78,3 +80,60 @@ def residual_encode_device(d_emb: int, n: int, d_centers: int, k: int, d_assign:
                            d_bad: int, stream: int = 0) -> None:
     """Device-pointer form of residual_to_q4_bytes; rows assigned past k set *d_bad."""
     check(lib.t5h_residual_encode_device(d_emb, n, d_centers, k, d_assign, d, d_codes, d_bad, stream or None))
+
+
+# ---- packed chunk embeddings (src/packops.rs:172-438) ------------------------------------
+
+def _rows_of(mats) -> tuple[np.ndarray, np.ndarray, int]:
+    mats = [np.ascontiguousarray(m, np.float32) for m in mats]
+    cols = mats[0].shape[1] if mats else 128
+    for m in mats:
+        if m.ndim != 2 or m.shape[1] != cols:
+            raise ValueError("every matrix must be 2-D with the same column count")
+    ro = np.zeros(len(mats) + 1, np.int32)
+    ro[1:] = np.cumsum([m.shape[0] for m in mats])
+    x = np.concatenate(mats, 0) if mats and ro[-1] > 0 else np.zeros((1, cols), np.float32)
+    return x, ro, cols
+
+
+def embeddings_to_packed_batch(mats, hip_device: int = 0, timing: bool = False):
+    """embeddings_to_packed of each [rows, cols] matrix (src/packops.rs:172-301), in one
+    batch on the GPU.  Returns the list of packed byte strings (and the device ms if timing)."""
+    x, ro, cols = _rows_of(mats)
+    B = len(ro) - 1
+    offs = np.zeros(B + 1, np.uint64)
+    cap = int(4 * B + (int(ro[-1]) // 1024 + B + 1) * (cols + 4 + 4 * 4096) + 2 * int(ro[-1]) * cols + 64)
+    out = np.empty(max(cap, 1), np.uint8)
+    ms = C.c_double(0.0)
+    check(lib.t5h_embeddings_to_packed(hip_device, x, ro, B, cols, out, cap, offs, C.byref(ms)))
+    res = [out[int(offs[b]):int(offs[b + 1])].tobytes() for b in range(B)]
+    return (res, ms.value) if timing else res
+
+
+def embeddings_to_packed(x: np.ndarray, hip_device: int = 0) -> bytes:
+    """TensorPackOps::embeddings_to_packed of one [rows, cols] matrix."""
+    return embeddings_to_packed_batch([x], hip_device)[0]
+
+
+def embeddings_from_packed_batch(bufs, cols: int = 128, hip_device: int = 0, timing: bool = False):
+    """embeddings_from_packed of each packed buffer (src/packops.rs:303-438): rows
+    L2-normalised.  Returns the list of [rows, cols] f32 arrays (and the device ms if timing)."""
+    B = len(bufs)
+    offs = np.zeros(B + 1, np.uint64)
+    offs[1:] = np.cumsum([len(b) for b in bufs])
+    buf = np.frombuffer(b"".join(bufs), np.uint8).copy() if offs[-1] else np.zeros(1, np.uint8)
+    rows = 0
+    for b in bufs:
+        if len(b) >= 4:
+            rows += int(np.frombuffer(b[:4], np.uint32)[0])
+    out = np.empty((max(rows, 1), cols), np.float32)
+    ro = np.zeros(B + 1, np.int32)
+    ms = C.c_double(0.0)
+    check(lib.t5h_embeddings_from_packed(hip_device, buf, offs, B, cols, out, rows, ro, C.byref(ms)))
+    res = [out[ro[b]:ro[b + 1]].copy() for b in range(B)]
+    return (res, ms.value) if timing else res
+
+
+def embeddings_from_packed(buf: bytes, cols: int = 128, hip_device: int = 0) -> np.ndarray:
+    """TensorPackOps::embeddings_from_packed of one packed buffer."""
+    return embeddings_from_packed_batch([buf], cols, hip_device)[0]
