@@ -431,23 +431,45 @@ __global__ __launch_bounds__(256) void pk_rans_enc(const uint16_t* __restrict__ 
       stage[i] = table[kk];
     }
     __syncthreads();
-    if (tid < 64) {
-      for (int i = 0; i < cn && !fail; i++) {
-        const EncSym e = stage[i];
-        const uint32_t freq = e.freq_shift & 0xffffu, shift = e.freq_shift >> 16;
-        const unsigned long long x_max = ((RANS_L >> RANS_BITS) << 32) * (unsigned long long)freq;
-        while (x >= x_max) {
-          if (cap_b - 4 * k < 4) {
-            fail = 1;
-            break;
-          }
-          if (tid == 0) out_words[cap_w - 1 - k] = (uint32_t)x;
-          k++;
-          x >>= 32;
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0 && !fail) {
+      // Wave 0 runs the coder; every value below is wave-uniform (parameters pass through
+      // readfirstlane), so the state lives in scalar registers and the loop branches on the
+      // scalar unit.  Parameters of the next 4 positions are read from LDS one group ahead.
+      EncSym nx[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) nx[j] = stage[min(j, cn - 1)];
+      bool ok = true;
+      for (int i = 0; i < cn && ok; i += 4) {
+        EncSym cu[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          cu[j] = nx[j];
+          nx[j] = stage[min(i + 4 + j, cn - 1)];
         }
-        const unsigned long long q = __umul64hi(x, e.rcp) >> shift;
-        x = x + e.bias + q * (unsigned long long)(RANS_TOTAL - freq);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (i + j >= cn || !ok) break;
+          const uint32_t fs = __builtin_amdgcn_readfirstlane(cu[j].freq_shift);
+          const uint32_t bias = __builtin_amdgcn_readfirstlane(cu[j].bias);
+          const uint32_t rlo = __builtin_amdgcn_readfirstlane((uint32_t)cu[j].rcp);
+          const uint32_t rhi = __builtin_amdgcn_readfirstlane((uint32_t)(cu[j].rcp >> 32));
+          const uint32_t freq = fs & 0xffffu, shift = fs >> 16;
+          const unsigned long long rcp = ((unsigned long long)rhi << 32) | rlo;
+          const unsigned long long x_max = (1ull << 51) * freq;  // ((L >> 12) << 32) * freq
+          while (x >= x_max) {
+            if (cap_b - 4 * k < 4) {
+              ok = false;
+              break;
+            }
+            if (tid == 0) out_words[cap_w - 1 - k] = (uint32_t)x;
+            k++;
+            x >>= 32;
+          }
+          const unsigned long long q = __umul64hi(x, rcp) >> shift;
+          x = x + bias + q * (unsigned long long)(RANS_TOTAL - freq);
+        }
       }
+      if (!ok && tid == 0) fail = 1;
     }
     __syncthreads();
   }
@@ -545,21 +567,29 @@ __global__ __launch_bounds__(256) void pk_rans_dec(const uint8_t* __restrict__ i
     }
   }
   __syncthreads();
+  // The stream, read 4 bytes at a time from any byte offset: two aligned dwords funnel-
+  // shifted (the input buffer carries 16 bytes of padding).  Addresses are wave-uniform.
   const uint8_t* d = in + w.data;
   const int clen = w.dlen;
+  auto word_at = [&](int p) -> uint32_t {
+    const uintptr_t a = (uintptr_t)(d + p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+    const unsigned long long two = ((unsigned long long)q[1] << 32) | q[0];
+    return (uint32_t)(two >> (8 * (a & 3)));
+  };
   float* dst = out + (size_t)w.row0 * cols;
-  unsigned long long x = 0;
+  unsigned long long x = ((unsigned long long)word_at(4) << 32) | word_at(0);
   int pos = 8;
-  bool bad = clen < 8;
-  if (!bad)
-    for (int k = 0; k < 8; k++) x |= (unsigned long long)d[k] << (8 * k);
+  bool bad = false;
+  uint32_t next = word_at(min(pos, clen - 4));  // prefetched renormalisation word
   // decode positions n-1 .. 0 in chunks of DEC_CHUNK (chunk j covers [hi - cn, hi))
   for (int hi = n; hi > 0; hi -= DEC_CHUNK) {
     const int cn = min(DEC_CHUNK, hi);
-    if (tid < 64 && !bad) {
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0 && !bad) {
+      // wave 0, wave-uniform state in scalar registers (table entries pass through readfirstlane)
       for (int i = cn - 1; i >= 0; i--) {
         const uint32_t c = (uint32_t)(x & (RANS_TOTAL - 1));
-        const uint32_t sf = cum_sf[c];
+        const uint32_t sf = __builtin_amdgcn_readfirstlane(cum_sf[c]);
         stage[i] = cum_v[c];
         x = (unsigned long long)(sf >> 16) * (x >> RANS_BITS) + c - (sf & 0xffffu);
         if (x < RANS_L) {
@@ -567,9 +597,9 @@ __global__ __launch_bounds__(256) void pk_rans_dec(const uint8_t* __restrict__ i
             bad = true;
             break;
           }
-          const uint32_t v = d[pos] | (d[pos + 1] << 8) | (d[pos + 2] << 16) | ((uint32_t)d[pos + 3] << 24);
+          x = (x << 32) | next;
           pos += 4;
-          x = (x << 32) | v;
+          next = word_at(min(pos, clen - 4));
           if (x < RANS_L) {
             bad = true;
             break;
