@@ -314,6 +314,49 @@ def test_gemv_matches_batched_gemm(xtr, xtr_gemm_only, L):
     assert np.array_equal(a, a2)  # deterministic split-K reduction
 
 
+def _handles_by_tail(enc_mod, img, cfg):
+    """Handles on one model with the batched GEMM's thin tail tiles off (T5H_GEMM_TAIL=0),
+    forced to 16 (1) and to 32 (2) token rows per math wave for the last row of full tiles."""
+    import os
+    hs = {}
+    for v in ("0", "1", "2"):
+        os.environ["T5H_GEMM_TAIL"] = v
+        try:
+            hs[v] = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+        finally:
+            del os.environ["T5H_GEMM_TAIL"]
+    return hs
+
+
+@pytest.mark.parametrize("layout", ["q4k", "hybrid"])
+def test_thin_tail_tiles_are_bit_identical(enc_mod, xtr, layout):
+    """Thin tail tiles run the same K order per output as full tiles: every tile plan gives the
+    same bits, through all 12 layers (Q4_K and f16 weights), with the chosen plan in between."""
+    cfg, img, gpu, _ = xtr
+    if layout == "hybrid":
+        img = synth.make_model(cfg, seed=3, layout="hybrid")
+        gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    hs = _handles_by_tail(enc_mod, img, cfg)
+    try:
+        rng = np.random.default_rng(77)
+        for lens in (rng.integers(32, 257, size=12), rng.integers(200, 257, size=21)):
+            cu = np.zeros(len(lens) + 1, np.int32)
+            cu[1:] = np.cumsum(lens)
+            assert cu[-1] % 256, "the batch must end in a partial row of tiles"
+            ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+            ref, _ = hs["0"].encode_packed(ids, cu)
+            for v in ("1", "2"):
+                got, _ = hs[v].encode_packed(ids, cu)
+                assert np.array_equal(got, ref), (layout, int(cu[-1]), v)
+            auto, _ = gpu.encode_packed(ids, cu)
+            assert np.array_equal(auto, ref), (layout, int(cu[-1]))
+    finally:
+        for h in hs.values():
+            h.close()
+        if layout == "hybrid":
+            gpu.close()
+
+
 @pytest.mark.parametrize("layout", ["q4k", "hybrid"])
 def test_gemv_small_model_layouts(enc_mod, layout):
     """d_model 256 / d_ff 512 (K = 256 and 512 splits) with Q4_K and f16 weights."""

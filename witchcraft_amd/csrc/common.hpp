@@ -83,7 +83,14 @@ __device__ __forceinline__ float gelu_tanh_dev(float x) {
 // Host-side launchers (defined in the .hip files) --------------------------------
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
-hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s);
+// Tile plan of one batched GEMM launch: full tiles of 64*mw token rows x bn weight rows
+// cover rows [0, m_main); thin tiles of 16*tail_mb rows per math wave cover [m_main, M)
+// (tail_mb = 0: full tiles everywhere).
+struct GemmPlan {
+  int mw = 4, bn = 128, m_main = 0, tail_mb = 0;
+};
+GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override);
+hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& plan, const GemmArgs& a, hipStream_t s);
 // Small-M variant (M <= GEMV_MAX_M tokens), same arguments and results.
 constexpr int GEMV_MAX_M = 64;
 hipError_t launch_gemv(int epi, int wfmt, const GemmArgs& a, hipStream_t s);

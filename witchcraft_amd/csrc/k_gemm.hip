@@ -121,24 +121,17 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
   }
 }
 
-template <int EPI, int WF, int MW, int BN, int S>
-__global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
-  constexpr int NP = 64 * MW, BM = 64 * MW, NB = BN / 16;
+// One output tile: tokens [m0, m0 + 16*MB*MW) x weight rows from n0.  MB = 16-row operand
+// blocks per math wave: 4 for full tiles, 1 or 2 for the thin tiles that spread the last,
+// partial round of a launch over every CU (the weight stage per K step is the same).
+template <int EPI, int WF, int MW, int BN, int S, int MB>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK]) {
+  constexpr int NP = 64 * MW, NB = BN / 16;
   // S register stages of A (math waves) and PB of raw weights (producers): the loads of a
   // step are issued S-1 (PB-1) steps before it is consumed, covering L2/MALL latency.
   // K / 64 is a multiple of S and of PB.
   constexpr int PB = 4;
   using R = BRaw<WF, NP, BN>;
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
-
-  // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous tile range.
-  const int per_xcd = gridDim.x / 8;
-  const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (tile >= tiles_m * tiles_n) return;
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
-  const int m0 = tm * BM;
-  const int n0 = tn * (EPI == EPI_GATED ? BN / 2 : BN);
   const int nkt = p.K / BK;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // waves [0, MW) compute, waves [MW, 2MW) produce; wave w runs on SIMD w % 4
@@ -170,22 +163,22 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
 
   // -------------------------------- math waves ---------------------------------
   const int lr = lane & 15, lg = lane >> 4;
-  // operand blocks of this wave's 4 row groups: block (rb, kb) at ((rb * K/32) + kb) * 512
+  // operand blocks of this wave's MB row groups: block (rb, kb) at ((rb * K/32) + kb) * 512
   const size_t kblk = p.K / 32;
-  const _Float16* ablk[4];
+  const _Float16* ablk[MB];
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++) ablk[mb] = p.A + ((size_t)((m0 + wave * 64) / 16 + mb) * kblk) * 512 + lane * 8;
+  for (int mb = 0; mb < MB; mb++) ablk[mb] = p.A + ((size_t)((m0 + wave * 16 * MB) / 16 + mb) * kblk) * 512 + lane * 8;
 
-  f4 acc[4][NB];
+  f4 acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < MB; i++)
 #pragma unroll
     for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   // A ring: step j in register stage j % S, loaded S-1 steps before it is used.
-  uint4 a[S][4][2];
+  uint4 a[S][MB][2];
 #define LOAD_A(st, kt)                                                                      \
-  _Pragma("unroll") for (int mb = 0; mb < 4; mb++) {                                        \
+  _Pragma("unroll") for (int mb = 0; mb < MB; mb++) {                                        \
     a[st][mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);     \
     a[st][mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512); \
   }
@@ -212,7 +205,7 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
           for (int nb = 0; nb < NB; nb++) {  // one weight fragment live at a time
             const h8 wf = *reinterpret_cast<const h8*>(bsrc + nb * 16 * LDSK + 32 * s);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++)
+            for (int mb = 0; mb < MB; mb++)
               acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, __builtin_bit_cast(h8, a[u][mb][s]),
                                                                     acc[mb][nb], 0, 0, 0);
           }
@@ -222,10 +215,10 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
   }
 #undef LOAD_A
 
-  // ---- epilogue: lane holds C[token m0+64w+16mb+lr][columns n0+16nb+4lg+0..3] ----
+  // ---- epilogue: lane holds C[token m0+16MB*w+16mb+lr][columns n0+16nb+4lg+0..3] ----
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++) {
-    const int m = m0 + wave * 64 + mb * 16 + lr;
+  for (int mb = 0; mb < MB; mb++) {
+    const int m = m0 + wave * 16 * MB + mb * 16 + lr;
     if (m >= p.M) continue;
     if constexpr (EPI == EPI_GATED) {
 #pragma unroll
@@ -238,30 +231,93 @@ void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
   }
 }
 
-template <int EPI, int WF, int BN, int S>
-hipError_t launch_s(int mw, const GemmArgs& a, hipStream_t s) {
-  const int cols = EPI == EPI_GATED ? BN / 2 : BN;
-  const int tiles_n = a.N / cols, tiles_m = (a.M + 64 * mw - 1) / (64 * mw);
-  const int grid = (tiles_m * tiles_n + 7) / 8 * 8;
-  if (mw == 2)
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 2, BN, S>), dim3(grid), dim3(256), 0, s, a, tiles_m, tiles_n);
-  else
-    hipLaunchKernelGGL((gemm_kernel<EPI, WF, 4, BN, S>), dim3(grid), dim3(512), 0, s, a, tiles_m, tiles_n);
+// Grid of one launch: blocks [0, main_blocks) run the full tiles of rows [0, m_main), the
+// rest the thin tiles (TMB row blocks per math wave) of rows [m_main, M).  Within each part,
+// block b runs on XCD b % 8 (workgroups are dealt round-robin), and each XCD gets a
+// contiguous range of tiles, so its L2 holds the A rows it streams plus the weights.
+struct GemmGrid {
+  int tiles_n, main_tiles, main_blocks, m_main, tail_tiles;
+};
+
+template <int EPI, int WF, int MW, int BN, int S, int TMB>
+__global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_kernel(GemmArgs p, GemmGrid g) {
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
+  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN;  // output columns per tile
+  int b = blockIdx.x;
+  if (TMB == 0 || b < g.main_blocks) {
+    const int tile = (b % 8) * (g.main_blocks / 8) + b / 8;
+    if (tile >= g.main_tiles) return;
+    gemm_tile<EPI, WF, MW, BN, S, 4>(p, (tile / g.tiles_n) * 64 * MW, (tile % g.tiles_n) * cols, Bs);
+  } else {
+    constexpr int MBT = TMB == 0 ? 1 : TMB;
+    b -= g.main_blocks;
+    const int tile = (b % 8) * (((int)gridDim.x - g.main_blocks) / 8) + b / 8;
+    if (tile >= g.tail_tiles) return;
+    gemm_tile<EPI, WF, MW, BN, S, MBT>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
+                                        (tile % g.tiles_n) * cols, Bs);
+  }
+}
+
+template <int EPI, int WF, int BN, int S, int MW, int TMB>
+hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
+  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = 64 * MW;
+  GemmGrid g;
+  g.tiles_n = a.N / cols;
+  g.m_main = TMB ? pl.m_main : a.M;
+  g.main_tiles = (g.m_main + bm - 1) / bm * g.tiles_n;
+  g.main_blocks = (g.main_tiles + 7) / 8 * 8;
+  const int bmt = 16 * (TMB ? TMB : 1) * MW;
+  g.tail_tiles = TMB ? (a.M - g.m_main + bmt - 1) / bmt * g.tiles_n : 0;
+  const int grid = g.main_blocks + (g.tail_tiles + 7) / 8 * 8;
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB>), dim3(grid), dim3(128 * MW), 0, s, a, g);
   return hipGetLastError();
 }
 
 // A prefetch depth 2 (one step ahead): deeper rings measured slower -- the A stream is
 // bound by L1/TA bandwidth, not latency, and more requests in flight only add contention.
 template <int EPI, int WF, int BN>
-hipError_t launch_cfg(int mw, const GemmArgs& a, hipStream_t s) {
-  return launch_s<EPI, WF, BN, 2>(mw, a, s);
+hipError_t launch_cfg(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
+  if (pl.mw == 2) return launch_plan<EPI, WF, BN, 2, 2, 0>(pl, a, s);
+  switch (pl.tail_mb) {
+    case 1: return launch_plan<EPI, WF, BN, 2, 4, 1>(pl, a, s);
+    case 2: return launch_plan<EPI, WF, BN, 2, 4, 2>(pl, a, s);
+    default: return launch_plan<EPI, WF, BN, 2, 4, 0>(pl, a, s);
+  }
 }
 
 template <int EPI>
-hipError_t launch_epi(int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s) {
+hipError_t launch_epi(int wfmt, const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (wfmt == WF_Q4K)
-    return bn == 64 ? launch_cfg<EPI, WF_Q4K, 64>(mw, a, s) : launch_cfg<EPI, WF_Q4K, 128>(mw, a, s);
-  return bn == 64 ? launch_cfg<EPI, WF_F16, 64>(mw, a, s) : launch_cfg<EPI, WF_F16, 128>(mw, a, s);
+    return pl.bn == 64 ? launch_cfg<EPI, WF_Q4K, 64>(pl, a, s) : launch_cfg<EPI, WF_Q4K, 128>(pl, a, s);
+  return pl.bn == 64 ? launch_cfg<EPI, WF_F16, 64>(pl, a, s) : launch_cfg<EPI, WF_F16, 128>(pl, a, s);
+}
+
+// Run time of the last tile when `tail` tiles of cost c follow `main` tiles of cost 1 on
+// `slots` workgroup slots, each tile taking the earliest free slot (the dispatcher's order).
+// After the main tiles, slots free up at r (slots - k of them) and r + 1 (k of them); the
+// tail tiles start at r + i*c and r + 1 + j*c, earliest first.
+double list_makespan(int main, int tail, double c, int slots) {
+  const int r = main / slots, k = main % slots;
+  double end = k ? r + 1 : r;
+  if (tail <= 0) return end;
+  const int n1 = slots - k, n2 = k;
+  int i = 0, j = 0, left = tail;
+  double start = r;
+  while (left > 0) {
+    const double t1 = r + i * c, t2 = n2 ? r + 1 + j * c : 1e30;
+    if (t1 <= t2) {
+      start = t1;
+      left -= n1;
+      i++;
+    } else {
+      start = t2;
+      left -= n2;
+      j++;
+    }
+  }
+  return start + c > end ? start + c : end;
 }
 
 }  // namespace
@@ -286,16 +342,62 @@ void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn) {
   }
 }
 
-hipError_t launch_gemm(int epi, int wfmt, int mw, int bn, const GemmArgs& a, hipStream_t s) {
+// Relative run time of a thin tile (16 or 32 token rows per math wave) against a full tile
+// of the same weight rows: the producers' weight unpacking per K step is the same, only the
+// MFMA work and the activation stream shrink.  Measured on MI355X as one round of 252 thin
+// tiles against one round of 252 full tiles, over the encoder's four weight shapes:
+// bn = 128: 0.45-0.55 (16 rows), 0.64-0.69 (32 rows); bn = 64: 0.50-0.61, 0.65-0.73.
+static double thin_tile_cost(int bn, int mb) {
+  if (bn == 128) return mb == 1 ? 0.53 : 0.68;
+  return mb == 1 ? 0.56 : 0.70;
+}
+
+// Full tiles for rows [0, m_main), thin tiles for the rest, where that shortens the launch:
+// with one workgroup per CU a launch of T full tiles takes ceil(T / CUs) rounds, and a last
+// round that is mostly empty costs as much as a full one.  Every split at a multiple of the
+// full tile height and both thin heights is evaluated with list_makespan.
+// tail_override: -1 = choose, 0 = full tiles only, 1 / 2 = thin tiles of that height for the
+// last row of full tiles (tests).
+GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override) {
+  GemmPlan pl;
+  gemm_pick_tile(M, n_rows, cus, pl.mw, pl.bn);
+  if (mw_override == 2 || mw_override == 4) pl.mw = mw_override;
+  if (bn_override == 64 || bn_override == 128) pl.bn = bn_override;
+  pl.m_main = M;
+  pl.tail_mb = 0;
+  if (pl.mw != 4 || M <= 0 || tail_override == 0) return pl;
+  const int bm = 256, tiles_n = n_rows / pl.bn, full = (M + bm - 1) / bm;
+  if (tail_override == 1 || tail_override == 2) {
+    pl.tail_mb = tail_override;
+    pl.m_main = (full - 1) * bm;
+    return pl;
+  }
+  double best = list_makespan(full * tiles_n, 0, 1.0, cus);
+  for (int j = full - 1; j >= 0; j--)
+    for (int mb = 1; mb <= 2; mb++) {
+      const int bmt = 64 * mb, tail = (M - j * bm + bmt - 1) / bmt * tiles_n;
+      const double t = list_makespan(j * tiles_n, tail, thin_tile_cost(pl.bn, mb), cus);
+      if (t < best - 1e-9) {
+        best = t;
+        pl.m_main = j * bm;
+        pl.tail_mb = mb;
+      }
+    }
+  return pl;
+}
+
+hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  if (mw != 2 && mw != 4) mw = 4;
+  if (pl.mw != 2 && pl.mw != 4) return hipErrorInvalidValue;
+  if (pl.tail_mb && (pl.mw != 4 || pl.m_main < 0 || pl.m_main % 256 || pl.m_main >= a.M))
+    return hipErrorInvalidValue;
   switch (epi) {
-    case EPI_F16: return launch_epi<EPI_F16>(wfmt, mw, bn, a, s);
-    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, mw, bn, a, s);
-    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, mw, bn, a, s);
-    case EPI_F32: return launch_epi<EPI_F32>(wfmt, mw, bn, a, s);
-    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, mw, bn, a, s);
-    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, mw, bn, a, s);
+    case EPI_F16: return launch_epi<EPI_F16>(wfmt, pl, a, s);
+    case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, pl, a, s);
+    case EPI_GATED: return launch_epi<EPI_GATED>(wfmt, pl, a, s);
+    case EPI_F32: return launch_epi<EPI_F32>(wfmt, pl, a, s);
+    case EPI_QKV: return launch_epi<EPI_QKV>(wfmt, pl, a, s);
+    case EPI_RELU: return launch_epi<EPI_RELU>(wfmt, pl, a, s);
   }
   return hipErrorInvalidValue;
 }

@@ -92,6 +92,7 @@ struct t5h_model {
   int gemm_mw_override = 0;  // T5H_GEMM_MW / T5H_GEMM_BN tuning knobs (0 = heuristic)
   bool batched_only = false;  // route every linear through the batched GEMM (t5h_ffn_block mode 1)
   int gemm_bn_override = 0;
+  int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail
 
   // ---- weights (one device arena) ----
   void* arena = nullptr;
@@ -414,11 +415,9 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
     return T5H_OK;
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
-  int mw, bn;
-  t5k::gemm_pick_tile(M, W.N * (W1 ? 2 : 1), m->cus, mw, bn);
-  if (m->gemm_mw_override) mw = m->gemm_mw_override;
-  if (m->gemm_bn_override) bn = m->gemm_bn_override;
-  HIP_OK(t5k::launch_gemm(epi, W.fmt, mw, bn, a, m->stream));
+  const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
+                                            m->gemm_bn_override, m->gemm_tail_override);
+  HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
   return T5H_OK;
 }
 
@@ -636,6 +635,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   if (const char* e = getenv("T5H_GEMM_BN")) {
     const int v = atoi(e);
     if (v == 64 || v == 128) m->gemm_bn_override = v;
+  }
+  if (const char* e = getenv("T5H_GEMM_TAIL")) {
+    const int v = atoi(e);
+    if (v >= 0 && v <= 2) m->gemm_tail_override = v;
   }
   const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
 
