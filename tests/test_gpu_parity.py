@@ -114,6 +114,16 @@ def test_small_model_ragged_batch(small):
     _check_batch(gpu, ora, ids, cu)
 
 
+def test_small_model_ragged_batch_past_four_key_tiles(small):
+    """5 to 8 key tiles of 64 per sequence: the attention's 4-slot load ring wraps part-way."""
+    cfg, _, gpu, ora = small
+    lens = [257, 300, 383, 420, 449, 512, 33]
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = np.random.default_rng(3).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    _check_batch(gpu, ora, ids, cu)
+
+
 def test_small_model_max_length_sequence(small):
     cfg, _, gpu, ora = small
     ids = np.random.default_rng(2).integers(1, cfg["vocab_size"], size=2048).astype(np.uint32)

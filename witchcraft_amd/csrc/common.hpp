@@ -72,6 +72,27 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   return (float)h;
 }
 
+// Cross-lane pairs without LDS (gfx950 v_permlane16_swap / v_permlane32_swap with the same
+// register as both operands): every lane l receives its own value and that of lane l ^ 16
+// (l ^ 32), in an order that differs between the two lanes of a pair -- so only commutative
+// combinations (+, max) are taken, and both lanes of a pair get identical bits.
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // candle Tensor::gelu (tanh form): 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
 // evaluated as the identical x * sigmoid(2u) = x / (1 + 2^(-2u log2 e)).
 __device__ __forceinline__ float gelu_tanh_dev(float x) {

@@ -27,6 +27,8 @@ constexpr int KT = 64;   // keys per tile
 constexpr int DK = 64;   // head dim (d_kv)
 constexpr int KPAD = DK + 8;
 constexpr int VPAD = KT + 8;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE = 5.5f;  // P <= e^5.5 < 256, far inside f16
 
 // Slot of key `key` (a multiple of 4) inside a tile row of Vt: key 16h + 4g + i of a 32-key
 // group sits at 8g + 4h + i, so keys {4g..4g+3, 16+4g..16+4g+3} -- the K-slots 8g..8g+7 of
@@ -115,36 +117,49 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
         s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
       }
     }
-    // bias + mask, running max
+    // bias, mask (only the last tile of a sequence has keys past L), running max
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) s[kb][i] += Bs[buf][bofs + kb * 16 + i];
+    if (k0 + KT > L) {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (k0 + kb * 16 + lg * 4 + i >= L) s[kb][i] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int j = k0 + kb * 16 + lg * 4 + i;
-        const float v = s[kb][i] + Bs[buf][bofs + kb * 16 + i];
-        s[kb][i] = j < L ? v : -INFINITY;
-        mx = fmaxf(mx, s[kb][i]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);  // finite: key k0 < L is always valid
-    const float corr = __expf(m_run - m_new);
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kb][i]);
+    mx = max_xor32(max_xor16(mx));
+    // The reference max moves only when a score exceeds it by more than RESCALE (or on the
+    // first tile, where m_run = -inf), so P <= e^RESCALE and the rescaling of O and l below
+    // is skipped for a whole wave on most tiles.  Same result up to rounding: P and l carry
+    // the same factor, divided out at the end.  mx is finite: key k0 < L is always valid.
+    const float m_new = mx > m_run + RESCALE ? mx : m_run;
+    // e^(v - m) = 2^(v log2e - m log2e): one FMA and one v_exp_f32 per score
+    const float mb = -m_new * LOG2E;
     float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float e = __expf(s[kb][i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], LOG2E, mb));
         s[kb][i] = e;
         rs += e;
       }
-    rs += __shfl_xor(rs, 16);
-    rs += __shfl_xor(rs, 32);
-    l_run = l_run * corr + rs;
-    m_run = m_new;
+    rs = sum_xor32(sum_xor16(rs));
+    if (__any(m_new != m_run)) {
+      const float corr = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, LOG2E, mb));  // 0 on the first tile
+      l_run *= corr;
 #pragma unroll
-    for (int db = 0; db < 4; db++) o[db] *= corr;
+      for (int db = 0; db < 4; db++) o[db] *= corr;
+    }
+    l_run += rs;
+    m_run = m_new;
 
     // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; K-slots 8lg..8lg+7 of step ks are
     // keys {32ks + 4lg + 0..3, 32ks + 16 + 4lg + 0..3} in both operands.

@@ -170,8 +170,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-      ssl[mt] += __shfl_xor(ssl[mt], 16);
-      ssl[mt] += __shfl_xor(ssl[mt], 32);
+      ssl[mt] = sum_xor32(sum_xor16(ssl[mt]));
       if (lg == 0) part[wave][mt * 16 + lr] = ssl[mt];
     }
     __syncthreads();

@@ -95,8 +95,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int kb = wave + 4 * RN_KEEP; live && kb < nblk; kb += 4)
     ss += sq4(*reinterpret_cast<const float4*>(xr + kb * 32)) +
           sq4(*reinterpret_cast<const float4*>(xr + kb * 32 + 4));
-  ss += __shfl_xor(ss, 16);
-  ss += __shfl_xor(ss, 32);
+  ss = sum_xor32(sum_xor16(ss));
   if (lane < 16) part[wave][lane] = ss;
   __syncthreads();
   const float tot = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
