@@ -121,6 +121,42 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
   }
 }
 
+// QKV epilogue through LDS (d_kv = 64).  The accumulators give each lane 4 columns of one
+// token, so direct stores into the head-major [3][H][tpad][64] layout write 16 x 32-byte
+// pieces per instruction.  Instead each 16-token block is staged in this wave's LDS region
+// (the weight stage, idle once the K loop has ended) and copied out as whole 128-byte head
+// rows, 16 bytes per lane.  `stage` holds 16 rows of BN + 8 halves.
+template <int BN, int MB>
+__device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, int n0, const f4 (&acc)[MB][BN / 16],
+                                                 _Float16* stage) {
+  constexpr int NB = BN / 16, RS = BN + 8;
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int inner = p.heads * 64;
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+      *reinterpret_cast<h4*>(stage + lr * RS + 16 * nb + 4 * lg) =
+          h4{(_Float16)acc[mb][nb][0], (_Float16)acc[mb][nb][1], (_Float16)acc[mb][nb][2], (_Float16)acc[mb][nb][3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int g = 0; g < BN / 64; g++) {
+      const int nn = n0 + 64 * g + p.n_off, which = nn / inner, h = (nn % inner) / 64;
+      _Float16* dst = (_Float16*)p.out + ((size_t)which * p.heads + h) * p.tpad * 64;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int c = lane + 64 * j, tok = c >> 3, part = c & 7;
+        const int m = mrow0 + 16 * mb + tok;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + tok * RS + 64 * g + 8 * part);
+        if (m < p.M) *reinterpret_cast<uint4*>(dst + (size_t)m * 64 + 8 * part) = v;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // One output tile: tokens [m0, m0 + 16*MB*MW) x weight rows from n0.  MB = 16-row operand
 // blocks per math wave: 4 for full tiles, 1 or 2 for the thin tiles that spread the last,
 // partial round of a launch over every CU (the weight stage per K step is the same).
@@ -216,6 +252,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
 #undef LOAD_A
 
   // ---- epilogue: lane holds C[token m0+16MB*w+16mb+lr][columns n0+16nb+4lg+0..3] ----
+  if constexpr (EPI == EPI_QKV) {
+    if (p.dkv == 64) {  // every 64-column group of the tile is one head: full-row stores
+      qkv_store_staged<BN, MB>(p, m0 + wave * 16 * MB, n0, acc, &Bs[0][0] + wave * (16 * (BN + 8)));
+      return;
+    }
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; mb++) {
     const int m = m0 + wave * 16 * MB + mb * 16 + lr;
