@@ -125,7 +125,9 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
 // token, so direct stores into the head-major [3][H][tpad][64] layout write 16 x 32-byte
 // pieces per instruction.  Instead each 16-token block is staged in this wave's LDS region
 // (the weight stage, idle once the K loop has ended) and copied out as whole 128-byte head
-// rows, 16 bytes per lane.  `stage` holds 16 rows of BN + 8 halves.
+// rows, 16 bytes per lane.  `stage` holds 16 rows of BN + 8 halves.  No wait is needed between
+// the staging writes and reads: a wave's LDS instructions execute in order, and the compiler
+// keeps the order of these possibly aliasing accesses.
 template <int BN, int MB>
 __device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, int n0, const f4 (&acc)[MB][BN / 16],
                                                  _Float16* stage) {
@@ -138,8 +140,6 @@ __device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, i
     for (int nb = 0; nb < NB; nb++)
       *reinterpret_cast<h4*>(stage + lr * RS + 16 * nb + 4 * lg) =
           h4{(_Float16)acc[mb][nb][0], (_Float16)acc[mb][nb][1], (_Float16)acc[mb][nb][2], (_Float16)acc[mb][nb][3]};
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int g = 0; g < BN / 64; g++) {
       const int nn = n0 + 64 * g + p.n_off, which = nn / inner, h = (nn % inner) / 64;
@@ -152,8 +152,6 @@ __device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, i
         if (m < p.M) *reinterpret_cast<uint4*>(dst + (size_t)m * 64 + 8 * part) = v;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
