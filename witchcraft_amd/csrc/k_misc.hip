@@ -68,27 +68,29 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                                                       _Float16* __restrict__ out, int T, int D,
                                                       float eps) {
   __shared__ float part[4][16];
+  // gamma of the kept blocks, staged once per workgroup: the per-lane gamma reads come from
+  // LDS instead of adding as many global loads as the x reads themselves
+  __shared__ __attribute__((aligned(16))) float gs[RN_KEEP * 4 * 32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 15, c8 = (lane >> 4) * 8;
   const int t = blockIdx.x * 16 + r;
   const bool live = t < T;
   const int nblk = D >> 5;
+  const int dk = D < RN_KEEP * 4 * 32 ? D : RN_KEEP * 4 * 32;  // gamma values staged
   const float* xr = x + (size_t)(live ? t : 0) * D + c8;
-  // x and gamma of the kept blocks are requested together: one memory round trip
-  float4 keep[RN_KEEP][2], gk[RN_KEEP][2];
+  // x of the kept blocks is requested at once: one memory round trip
+  float4 keep[RN_KEEP][2];
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
     const int kb = wave + 4 * j;
-    keep[j][0] = keep[j][1] = gk[j][0] = gk[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (kb < nblk) {
-      gk[j][0] = *reinterpret_cast<const float4*>(w + kb * 32 + c8);
-      gk[j][1] = *reinterpret_cast<const float4*>(w + kb * 32 + c8 + 4);
-      if (live) {
-        keep[j][0] = *reinterpret_cast<const float4*>(xr + kb * 32);
-        keep[j][1] = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
-      }
+    keep[j][0] = keep[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (kb < nblk && live) {
+      keep[j][0] = *reinterpret_cast<const float4*>(xr + kb * 32);
+      keep[j][1] = *reinterpret_cast<const float4*>(xr + kb * 32 + 4);
     }
   }
+  for (int i = threadIdx.x * 4; i < dk; i += 256 * 4)
+    *reinterpret_cast<float4*>(gs + i) = *reinterpret_cast<const float4*>(w + i);
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) ss += sq4(keep[j][0]) + sq4(keep[j][1]);
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
           sq4(*reinterpret_cast<const float4*>(xr + kb * 32 + 4));
   ss = sum_xor32(sum_xor16(ss));
   if (lane < 16) part[wave][lane] = ss;
-  __syncthreads();
+  __syncthreads();  // also publishes gs
   const float tot = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
   const float inv = 1.0f / sqrtf(tot / (float)D + eps);
   _Float16* ob = out + (size_t)blockIdx.x * nblk * 512 + lane * 8;
@@ -111,7 +113,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
     const int kb = wave + 4 * j;
-    if (kb < nblk) emit(kb, keep[j][0], keep[j][1], gk[j][0], gk[j][1]);
+    if (kb < nblk)
+      emit(kb, keep[j][0], keep[j][1], *reinterpret_cast<const float4*>(gs + kb * 32 + c8),
+           *reinterpret_cast<const float4*>(gs + kb * 32 + c8 + 4));
   }
   for (int kb = wave + 4 * RN_KEEP; kb < nblk; kb += 4) {
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
