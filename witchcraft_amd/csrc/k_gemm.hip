@@ -46,7 +46,10 @@ __device__ __forceinline__ void brow(int r, int n0, const GemmArgs& p, const voi
   }
 }
 
-// Raw weights of one K step held by a producer thread between load and unpack.
+// Raw weights of one K step held by a producer thread between load and unpack.  The f16
+// chunks use a native vector type: arrays of HIP's uint4 (a union) in this ring are not
+// promoted to registers and end up in scratch memory.
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 template <int WF, int NP, int BN>
 struct BRaw {
   static constexpr int TPR = NP / BN;   // producer threads per weight row (Q4_K)
@@ -55,7 +58,7 @@ struct BRaw {
   static constexpr int F16_LOADS = BN * BK * 2 / 16 / NP;
   uint4 hd;
   uint32_t q[NQ];
-  uint4 f[WF == WF_F16 ? F16_LOADS : 1];
+  u4v f[WF == WF_F16 ? F16_LOADS : 1];
 };
 
 template <int EPI, int WF, int NP, int BN>
@@ -88,7 +91,7 @@ __device__ __forceinline__ void load_b(BRaw<WF, NP, BN>& br, const GemmArgs& p, 
       const void* W;
       int n;
       brow<EPI, BN>(r, n0, p, W, n);
-      br.f[i] = *reinterpret_cast<const uint4*>((const _Float16*)W + (size_t)n * p.K + kt * BK + c8);
+      br.f[i] = *reinterpret_cast<const u4v*>((const _Float16*)W + (size_t)n * p.K + kt * BK + c8);
     }
   }
 }
@@ -116,7 +119,7 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
 #pragma unroll
     for (int i = 0; i < R::F16_LOADS; i++) {
       const int idx = i * NP + pt, r = idx >> 3, c8 = (idx & 7) * 8;
-      *reinterpret_cast<uint4*>(Bs + r * LDSK + c8) = br.f[i];
+      *reinterpret_cast<u4v*>(Bs + r * LDSK + c8) = br.f[i];
     }
   }
 }
