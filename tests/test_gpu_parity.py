@@ -324,6 +324,24 @@ def test_gemv_matches_batched_gemm(xtr, xtr_gemm_only, L):
     assert np.array_equal(a, a2)  # deterministic split-K reduction
 
 
+def test_sequence_output_independent_of_batch_neighbours(xtr):
+    """A sequence's embeddings are bit-identical whether it is encoded inside a packed batch or
+    alone: rows past a sequence's end (the next sequence's data inside a batch) must not leak
+    into attention, and every GEMM tile plan keeps the same K order per output.  Sequences are
+    longer than the GEMV cutoff so that both runs take the batched path."""
+    cfg, _, gpu, _ = xtr
+    rng = np.random.default_rng(21)
+    lens = rng.integers(65, 300, size=10)
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    out, _ = gpu.encode_packed(ids, cu)
+    for b in range(len(lens)):
+        s, e = int(cu[b]), int(cu[b + 1])
+        one, _ = gpu.encode_packed(ids[s:e], np.array([0, e - s], np.int32))
+        assert np.array_equal(out[s:e], one), (b, e - s, float(np.abs(out[s:e] - one).max()))
+
+
 def _handles_by_tail(enc_mod, img, cfg):
     """Handles on one model with the batched GEMM's thin tail tiles off (T5H_GEMM_TAIL=0),
     forced to 16 (1) and to 32 (2) token rows per math wave for the last row of full tiles."""

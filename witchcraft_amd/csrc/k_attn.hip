@@ -153,7 +153,9 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
       }
     rs = sum_xor32(sum_xor16(rs));
     if (__any(m_new != m_run)) {
-      const float corr = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, LOG2E, mb));  // 0 on the first tile
+      // exactly 1 for lanes whose max did not move (the wave-wide test also sees padding
+      // queries, which must not perturb real ones); 0 on the first tile (m_run = -inf)
+      const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
       l_run *= corr;
 #pragma unroll
       for (int db = 0; db < 4; db++) o[db] *= corr;
