@@ -82,6 +82,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
   const int nw = blockDim.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
+  const int tb0 = blockIdx.y * MT;  // first 16-token block of this workgroup
   const int kw = p.K / nw, kbeg = wave * kw, nch = kw / 64;
   const size_t kblk = p.K / 32;
   const _Float16* xa = p.A + lane * 8;  // operand block (mt, kb) at (mt * K/32 + kb) * 512
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
           gv[c][s][0] = *reinterpret_cast<const float4*>(p.gamma + kk);                        \
           gv[c][s][1] = *reinterpret_cast<const float4*>(p.gamma + kk + 4);                    \
           _Pragma("unroll") for (int mt = 0; mt < MT; mt++) {                                  \
-            const int t = mt * 16 + lr;                                                        \
+            const int t = (tb0 + mt) * 16 + lr;                                                \
             xv[c][s][mt][0] = xv[c][s][mt][1] = make_float4(0.f, 0.f, 0.f, 0.f);               \
             if (t < p.M) {                                                                     \
               xv[c][s][mt][0] = *reinterpret_cast<const float4*>(p.xf + (size_t)t * p.K + kk);     \
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
           }                                                                                    \
         } else {                                                                               \
           _Pragma("unroll") for (int mt = 0; mt < MT; mt++)                                    \
-              xr[c][s][mt] = *reinterpret_cast<const uint4*>(xa + ((size_t)mt * kblk + k / 32 + s) * 512); \
+              xr[c][s][mt] = *reinterpret_cast<const uint4*>(xa + ((size_t)(tb0 + mt) * kblk + k / 32 + s) * 512); \
         }                                                                                      \
       }                                                                                        \
     }                                                                                          \
@@ -131,8 +132,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
   // Residual epilogue: fetch this lane's x quad now, so the add does not wait on memory.
   float4 xres = make_float4(0.f, 0.f, 0.f, 0.f);
   if constexpr (EPI == EPI_RESID) {
-    if (wave < MT && wave * 16 + lr < p.M)
-      xres = *reinterpret_cast<const float4*>((const float*)p.out + (size_t)(wave * 16 + lr) * p.ldo + n0 + 4 * lg);
+    if (wave < MT && (tb0 + wave) * 16 + lr < p.M)
+      xres = *reinterpret_cast<const float4*>((const float*)p.out + (size_t)((tb0 + wave) * 16 + lr) * p.ldo + n0 + 4 * lg);
   }
 
   // Fused T5LayerNorm (src/quantized_t5.rs:162-173): 1 / sqrt(mean(x^2) + eps) per token.
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
         for (int s = 0; s < 2; s++)
 #pragma unroll
           for (int mt = 0; mt < MT; mt++) {
-            const int t = mt * 16 + lr;
+            const int t = (tb0 + mt) * 16 + lr;
             if (t < p.M) {
               const float* xp = p.xf + (size_t)t * p.K + kbeg + 64 * c + 32 * s + 8 * lg;
               ssl[mt] += sq(*reinterpret_cast<const float4*>(xp)) + sq(*reinterpret_cast<const float4*>(xp + 4));
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
       v[g] = red[(g * MT + mt) * 64 + lane];
       for (int w = 1; w < nw; w++) v[g] += red[((w * G + g) * MT + mt) * 64 + lane];
     }
-    const int m = mt * 16 + lr;
+    const int m = (tb0 + mt) * 16 + lr;
     if (m >= p.M) continue;
     if constexpr (EPI == EPI_GATED) {
       store_quad_gated(p, m, n0 + 4 * lg, v[0], v[G - 1]);
@@ -270,22 +271,23 @@ hipError_t launch_mt(const GemmArgs& a, hipStream_t s) {
   constexpr bool WIDE = G * MT * 12 <= 64 && !(NORM && MT == 4);
   const int nw = gemv_waves(a.K, G, MT, WIDE ? 16 : 8);
   const size_t lds = (size_t)nw * G * MT * 64 * sizeof(f4);
+  const dim3 grid(a.N / 16, (a.M + 16 * MT - 1) / (16 * MT));
   if constexpr (WIDE) {
     if (nw > 8) {
-      hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 1024>), dim3(a.N / 16), dim3(64 * nw), lds, s, a);
+      hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 1024>), grid, dim3(64 * nw), lds, s, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 512>), dim3(a.N / 16), dim3(64 * nw), lds, s, a);
+  hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 512>), grid, dim3(64 * nw), lds, s, a);
   return hipGetLastError();
 }
 
+// One workgroup per 16 weight rows and 16 tokens: every workgroup streams the activations of
+// its own 16 tokens only, which is what bounds these launches (each CU receives activation
+// bytes at a fixed rate), while the weight rows are re-read per token block from L2.
 template <int EPI, int WF, bool NORM>
 hipError_t launch_wf(const GemmArgs& a, hipStream_t s) {
-  const int mt = (a.M + 15) / 16;
-  if (mt == 1) return launch_mt<EPI, WF, 1, NORM>(a, s);
-  if (mt == 2) return launch_mt<EPI, WF, 2, NORM>(a, s);
-  return launch_mt<EPI, WF, 4, NORM>(a, s);
+  return launch_mt<EPI, WF, 1, NORM>(a, s);
 }
 
 template <int EPI>
