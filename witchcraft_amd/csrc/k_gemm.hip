@@ -434,6 +434,9 @@ hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a,
   if (pl.mw != 2 && pl.mw != 4) return hipErrorInvalidValue;
   if (pl.tail_mb && (pl.mw != 4 || pl.m_main < 0 || pl.m_main % 256 || pl.m_main >= a.M))
     return hipErrorInvalidValue;
+  if (pl.bn != 64 && pl.bn != 128) return hipErrorInvalidValue;
+  // whole tiles along N and whole 4-step rings of 64-wide K steps
+  if (a.N % (epi == EPI_GATED ? pl.bn / 2 : pl.bn) || a.K % 256) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_F16: return launch_epi<EPI_F16>(wfmt, pl, a, s);
     case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, pl, a, s);
