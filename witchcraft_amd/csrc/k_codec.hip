@@ -37,11 +37,15 @@ using t5k::Q4Table;
 typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kBufDword3 = 0x00020000;  // raw buffer descriptor word 3: 32-bit data, OOB -> 0
 
-__device__ __forceinline__ uint32_t q4_code(float r, const Q4Ladder& lad) {
-  uint32_t q = 0;
-#pragma unroll
-  for (int j = 0; j < 15; j++) q += r >= lad.t[j] ? 1u : 0u;
-  return q;
+// The code of r: the number of thresholds t[0..14] (strictly increasing) at or below r, found
+// by bisection -- 4 compares instead of 15.  code >= 8 iff r >= t[7]; then, from base i,
+// code >= i + 4 iff r >= t[i + 3], and so on.  NaN compares false everywhere: code 0.
+__device__ __forceinline__ uint32_t q4_code(float r, const float* t, float t7) {
+  uint32_t i = r >= t7 ? 8u : 0u;
+  i += r >= t[i + 3] ? 4u : 0u;
+  i += r >= t[i + 1] ? 2u : 0u;
+  i += r >= t[i] ? 1u : 0u;
+  return i;
 }
 
 // One thread per 8 values (4 code bytes) of a row; D % 8 == 0.  Rows whose assignment is out
@@ -51,6 +55,9 @@ __global__ __launch_bounds__(256) void residual_encode_kernel(const float* __res
                                                               const uint32_t* __restrict__ assign, int N, int D,
                                                               int K, Q4Ladder lad, uint8_t* __restrict__ out,
                                                               unsigned* __restrict__ bad) {
+  __shared__ float tl[16];
+  if (threadIdx.x < 15) tl[threadIdx.x] = lad.t[threadIdx.x];
+  __syncthreads();
   const int groups = D / 8;
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (size_t)N * groups) return;
@@ -60,9 +67,10 @@ __global__ __launch_bounds__(256) void residual_encode_kernel(const float* __res
   if (a < (uint32_t)K) {
     const float* e = emb + (size_t)row * D + 8 * g;
     const float* c = centers + (size_t)a * D + 8 * g;
+    const float t7 = lad.t[7];
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      const uint32_t hi = q4_code(e[j] - c[j], lad), lo = q4_code(e[j + 1] - c[j + 1], lad);
+      const uint32_t hi = q4_code(e[j] - c[j], tl, t7), lo = q4_code(e[j + 1] - c[j + 1], tl, t7);
       word |= ((hi << 4) | lo) << (4 * j);  // byte j/2: value j in the high nibble
     }
   } else if (g == 0) {
