@@ -233,6 +233,21 @@ def test_hybrid_layout_f32_attention_weights(enc_mod):
     _check_batch(gpu, ora, ids, cu)
 
 
+def test_xtr_hybrid_layout_large_batch_vs_oracle(enc_mod):
+    """cfg5's layout at XTR-base size, with a batch (~2,000 tokens) large enough for the full
+    4-wave x 128-row tiles and thin tails of the f16-weight GEMMs (q/k/v/o/wo)."""
+    cfg = dict(synth.XTR_BASE)
+    img = synth.make_model(cfg, seed=41, layout="hybrid")
+    gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    try:
+        ora = orc.OracleModel(img, cfg)
+        ids, cu = synth.ragged_batch(12, 100, 256, cfg["vocab_size"], seed=14)
+        assert cu[-1] > 1500
+        _check_batch(gpu, ora, ids, cu)
+    finally:
+        gpu.close()
+
+
 def test_q4k_embedding_table(enc_mod):
     cfg = synth.small_config()
     img = synth.make_model(cfg, seed=41, emb_format="q4k")
