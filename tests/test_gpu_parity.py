@@ -137,6 +137,15 @@ def test_xtr_cfg2_sample_vs_oracle(xtr):
     _check_batch(gpu, ora, ids, cu)
 
 
+def test_xtr_cfg4_lengths_vs_oracle(xtr):
+    """Sequences of the bulk config's upper range (400-512 tokens, 7-8 key tiles) in a ~2,300-token
+    batch: full GEMM tiles, thin tails and long attention rows, every sequence against the oracle."""
+    cfg, _, gpu, ora = xtr
+    ids, cu = synth.ragged_batch(5, 400, 512, cfg["vocab_size"], seed=15)
+    assert cu[-1] > 1500
+    _check_batch(gpu, ora, ids, cu)
+
+
 def test_xtr_query_shape_vs_oracle(xtr):
     """cfg3: batch 1, 32 tokens."""
     cfg, _, gpu, ora = xtr
