@@ -422,3 +422,75 @@ def test_gemv_small_model_layouts(enc_mod, layout):
         ids = np.random.default_rng(sum(lens)).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
         _check_batch(gpu, ora, ids, cu)
     gpu.close()
+
+
+def _handle_with_env(enc_mod, img, cfg, **env):
+    """A model handle created with the given T5H_* tuning variables set."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("layout", ["q4k", "hybrid"])
+def test_folded_norm_matches_standalone_norm(enc_mod, xtr, layout):
+    """On the batched path every T5LayerNorm after the first is folded into the GEMMs beside it:
+    the residual GEMM stores f16(x * gamma * s) and per-tile sums of x^2, and the next GEMM
+    scales its result by rsqrt(mean(x^2) + eps) / s.  Against standalone RMSNorm launches
+    (T5H_FOLD_NORM=0) the outputs agree at f16 operand precision, and both meet the oracle bar."""
+    cfg, img, gpu, ora = xtr
+    own = layout == "hybrid"
+    if own:
+        img = synth.make_model(cfg, seed=3, layout="hybrid")
+        gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+        ora = orc.OracleModel(img, cfg)
+    unfolded = _handle_with_env(enc_mod, img, cfg, T5H_FOLD_NORM="0")
+    try:
+        ids, cu = synth.ragged_batch(24, 32, 256, cfg["vocab_size"], seed=5)
+        a, na = gpu.encode_packed(ids, cu)
+        b, nb = unfolded.encode_packed(ids, cu)
+        assert np.isfinite(a).all()
+        assert rel(a, b) <= CROSS_PATH_REL, rel(a, b)
+        assert cos_rows(a, b).min() >= 0.9999
+        for s_, e_ in ((0, 1), (7, 8), (23, 24)):
+            s, e = int(cu[s_]), int(cu[e_])
+            ref = ora.forward(ids[s:e])
+            assert cos_rows(a[s:e], ref).min() >= COS_MIN
+            assert cos_rows(b[s:e], ref).min() >= COS_MIN
+    finally:
+        unfolded.close()
+        if own:
+            gpu.close()
+
+
+def test_folded_norm_survives_residual_growth(enc_mod):
+    """The folded norm stores the next operand with a scale taken from the previous norm, so a
+    residual stream that grows by orders of magnitude between two norms must still fit f16: here
+    the first FFN grows the residual RMS from ~1 to ~1.7e4 (wo std 2000).  4 layers, against the
+    oracle and against standalone norms."""
+    cfg = dict(synth.XTR_BASE, num_layers=4)
+    img = synth.make_model(cfg, seed=9, std_over={"DenseReluDense.wo": 2000.0})
+    gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    unfolded = _handle_with_env(enc_mod, img, cfg, T5H_FOLD_NORM="0")
+    ora = orc.OracleModel(img, cfg)
+    try:
+        ids, cu = synth.ragged_batch(6, 70, 200, cfg["vocab_size"], seed=12)
+        a, _ = gpu.encode_packed(ids, cu)
+        b, _ = unfolded.encode_packed(ids, cu)
+        assert np.isfinite(a).all()
+        assert cos_rows(a, b).min() >= 0.9999
+        for k in range(6):
+            s, e = int(cu[k]), int(cu[k + 1])
+            x_last = ora.hidden(ids[s:e], 3)  # input of the last block: the grown residual
+            assert np.sqrt((x_last.astype(np.float64) ** 2).mean()) > 1e3
+            assert cos_rows(a[s:e], ora.forward(ids[s:e])).min() >= COS_MIN, k
+    finally:
+        unfolded.close()
+        gpu.close()

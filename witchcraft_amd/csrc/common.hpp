@@ -20,7 +20,7 @@ enum EmbFmt : int { EMB_F32 = 0, EMB_Q4K = 1 };
 // GEMM epilogues.
 enum Epilogue : int {
   EPI_F16 = 0,    // out f16 [M][ldo] in operand order (tiled_index)
-  EPI_RESID = 1,  // resid f32 [M][ldo] += acc
+  EPI_RESID = 1,  // resid f32 [M][ldo] += acc; the batched GEMM reads (not writes) rows up to Mpad
   EPI_GATED = 2,  // out f16 = gelu_tanh(acc(W0)) * acc(W1), operand order
   EPI_F32 = 3,    // out f32 [M][ldo]
   EPI_QKV = 4,    // q/k/v f16 head-major [3][H][tpad][dkv]
@@ -52,7 +52,37 @@ struct GemmArgs {
   const float* xf;
   const float* gamma;
   float eps;
+  // Batched GEMM only: T5LayerNorm folded into the GEMMs on either side of it.  Each token
+  // has a 64-byte record rec[16m .. 16m+15]: slots t < 15 hold sums of x^2 over the columns
+  // [64t, 64t + 64) (slots past D/64 stay zero), slot 15 the power of two s with which the
+  // f16 operand of that token was stored.
+  //  * producer (EPI_RESID with nx set): x += acc as usual; then nx = f16(x * ngamma * s) in
+  //    operand order with s = rec[16m + 15], and each tile's sums of x^2 into rec.
+  //  * consumer (any other epilogue with rec set): the operand is f16(x * gamma * s), so acc
+  //    is scaled by rsqrt(mean(x^2) + eps) / s; the tile at n0 = 0 writes the s of the next
+  //    producer, a power of two near 1/16 of that inverse RMS, into rec_next[16m + 15].
+  float* rec;
+  float* rec_next;
+  _Float16* nx;
+  const float* ngamma;
 };
+
+// Largest row length (d_model) whose sums of squares fit a norm record (15 slots of 64).
+constexpr int NORM_REC_MAX_D = 15 * 64;
+
+// The operand scale that follows an inverse RMS: the power of two at or below inv, / 16.
+// Stored values then have an RMS near |gamma| / 16, leaving room for the residual stream to
+// grow before the next norm; 1 when inv is 0, subnormal, infinite or NaN.
+__host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
+  uint32_t b;
+  __builtin_memcpy(&b, &inv, 4);
+  const uint32_t e = b & 0x7f800000u;
+  uint32_t r = 0x3f800000u;
+  if (e > (4u << 23) && e < 0x7f800000u) r = e - (4u << 23);
+  float s;
+  __builtin_memcpy(&s, &r, 4);
+  return s;
+}
 
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]
@@ -119,8 +149,9 @@ void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
                         float* x, unsigned* err_flag, hipStream_t s);
+// rec: when set, record mode for a consuming GEMM that folds the norm (GemmArgs::rec).
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
-                          hipStream_t s);
+                          hipStream_t s, float* rec = nullptr);
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s);
 // Query-side scoring: C = A . B^T (f32) and its per-row argmax (k_score.hip).

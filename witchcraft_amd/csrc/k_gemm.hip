@@ -158,6 +158,112 @@ __device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, i
   }
 }
 
+// Residual epilogue x += acc; with GemmArgs::nx set it also prepares the next T5LayerNorm:
+// the f16 operand f16(x * gamma * s) in operand order and the tile's sums of x^2 per 64-column
+// group in the token's norm record.  Lane (lr, lg) holds columns n0 + 16nb + 4lg .. +3 of token
+// mrow0 + 16mb + lr, so a group's sum is the lane's 16 squares plus those of the lanes lr + 16,
+// lr + 32, lr + 48 (xor 16, xor 32).  Every load is unconditional -- x and the records have
+// Mpad rows, so rows past M read padding -- and the x reads of CH row blocks are issued
+// together: a guarded load per quad would cost one memory round trip each.  Only the stores
+// are guarded; rows past M take part in the sums but store nothing.
+template <int BN, int MB>
+__device__ __forceinline__ void resid_store_tile(const GemmArgs& p, int mrow0, int n0, const f4 (&acc)[MB][BN / 16]) {
+  constexpr int NB = BN / 16, G = BN / 64;
+  constexpr int CH = BN == 64 ? MB : (MB >= 2 ? 2 : 1);  // row blocks whose x is read at once
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const bool fold = p.nx != nullptr;
+  float* x = (float*)p.out;
+  float4 g[NB];
+  float s[MB], ss[MB][G];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+    for (int j = 0; j < G; j++) ss[mb][j] = 0.f;
+    s[mb] = 0.f;
+  }
+  if (fold) {
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) g[nb] = *reinterpret_cast<const float4*>(p.ngamma + n0 + 16 * nb + 4 * lg);
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) s[mb] = p.rec[(size_t)(mrow0 + 16 * mb + lr) * 16 + 15];
+  }
+#pragma unroll
+  for (int c0 = 0; c0 < MB; c0 += CH) {
+    float4 xv[CH][NB];
+#pragma unroll
+    for (int j = 0; j < CH; j++)
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++)
+        xv[j][nb] = *reinterpret_cast<const float4*>(x + (size_t)(mrow0 + 16 * (c0 + j) + lr) * p.ldo + n0 +
+                                                     16 * nb + 4 * lg);
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+      const int mb = c0 + j, m = mrow0 + 16 * mb + lr;
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        float4& r = xv[j][nb];
+        r.x += acc[mb][nb][0];
+        r.y += acc[mb][nb][1];
+        r.z += acc[mb][nb][2];
+        r.w += acc[mb][nb][3];
+        ss[mb][nb / 4] += (r.x * r.x + r.y * r.y) + (r.z * r.z + r.w * r.w);
+      }
+      if (m < p.M) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+          const int n = n0 + 16 * nb + 4 * lg;
+          const float4 r = xv[j][nb];
+          *reinterpret_cast<float4*>(x + (size_t)m * p.ldo + n) = r;
+          if (fold)
+            *reinterpret_cast<h4*>(p.nx + tiled_index(m, n, p.ldo)) =
+                h4{(_Float16)((r.x * g[nb].x) * s[mb]), (_Float16)((r.y * g[nb].y) * s[mb]),
+                   (_Float16)((r.z * g[nb].z) * s[mb]), (_Float16)((r.w * g[nb].w) * s[mb])};
+        }
+      }
+    }
+  }
+  if (fold) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const int m = mrow0 + 16 * mb + lr;
+#pragma unroll
+      for (int j = 0; j < G; j++) {
+        const float t = sum_xor32(sum_xor16(ss[mb][j]));
+        if (m < p.M && lg == 0) p.rec[(size_t)m * 16 + n0 / 64 + j] = t;
+      }
+    }
+  }
+}
+
+// Consumer side of a folded T5LayerNorm (GemmArgs::rec).  Lane l serves token
+// mrow0 + 16 * (l / 16) + l % 16 (lanes whose row block lies past MB read block 0 instead):
+// norm_rec_load fetches its record before the K loop's first loads, norm_factor turns it
+// into rsqrt(mean(x^2) + eps) / s once those have landed.  The sums run in a fixed order, so
+// every tile of every launch gets the same bits.  Tiles at n0 = 0 also store the next
+// producer's operand scale.
+template <int MB>
+__device__ __forceinline__ int norm_row(int mrow0) {
+  const int lane = threadIdx.x & 63, mb = lane >> 4;
+  return mrow0 + 16 * (mb < MB ? mb : 0) + (lane & 15);
+}
+template <int MB>
+__device__ __forceinline__ void norm_rec_load(const GemmArgs& p, int mrow0, float4 (&r)[4]) {
+  const float4* src = reinterpret_cast<const float4*>(p.rec + (size_t)norm_row<MB>(mrow0) * 16);
+#pragma unroll
+  for (int i = 0; i < 4; i++) r[i] = src[i];
+}
+template <int MB>
+__device__ __forceinline__ float norm_factor(const GemmArgs& p, int mrow0, int n0, const float4 (&r)[4]) {
+  const float4 a = r[0], b = r[1], c = r[2], d = r[3];
+  const float tot = (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) +
+                    (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + d.z));
+  const float inv = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+  const int m = norm_row<MB>(mrow0);
+  if (p.rec_next && n0 == 0 && (threadIdx.x & 63) < 16 * MB && m < p.M)
+    p.rec_next[(size_t)m * 16 + 15] = norm_operand_scale(inv);
+  return inv / d.w;
+}
+
 // One output tile: tokens [m0, m0 + 16*MB*MW) x weight rows from n0.  MB = 16-row operand
 // blocks per math wave: 4 for full tiles, 1 or 2 for the thin tiles that spread the last,
 // partial round of a launch over every CU (the weight stage per K step is the same).
@@ -212,6 +318,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
 #pragma unroll
     for (int j = 0; j < NB; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
+  // folded T5LayerNorm: the records are requested ahead of the first A loads
+  const bool fold = EPI != EPI_RESID && p.rec != nullptr;
+  float4 nrec[4];
+  if (fold) norm_rec_load<MB>(p, m0 + wave * 16 * MB, nrec);
+  __builtin_amdgcn_sched_barrier(0);
+
   // A ring: step j in register stage j % S, loaded S-1 steps before it is used.
   uint4 a[S][MB][2];
 #define LOAD_A(st, kt)                                                                      \
@@ -224,6 +336,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
     LOAD_A(i, i);
     __builtin_amdgcn_sched_barrier(0);  // stages issued in order
   }
+  const float fs = fold ? norm_factor<MB>(p, m0 + wave * 16 * MB, n0, nrec) : 1.f;
   __syncthreads();
 
   // nkt % S == 0 (K % 256 == 0); as in the producers, loads past the end are clamped
@@ -253,6 +366,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
 #undef LOAD_A
 
   // ---- epilogue: lane holds C[token m0+16MB*w+16mb+lr][columns n0+16nb+4lg+0..3] ----
+  if constexpr (EPI == EPI_RESID) {
+    resid_store_tile<BN, MB>(p, m0 + wave * 16 * MB, n0, acc);
+    return;
+  } else if (fold) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const float f = __shfl(fs, mb * 16 + lr);
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) acc[mb][nb] *= f;
+    }
+  }
   if constexpr (EPI == EPI_QKV) {
     if (p.dkv == 64) {  // every 64-column group of the tile is one head: full-row stores
       qkv_store_staged<BN, MB>(p, m0 + wave * 16 * MB, n0, acc, &Bs[0][0] + wave * (16 * (BN + 8)));
@@ -437,6 +561,10 @@ hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a,
   if (pl.bn != 64 && pl.bn != 128) return hipErrorInvalidValue;
   // whole tiles along N and whole 4-step rings of 64-wide K steps
   if (a.N % (epi == EPI_GATED ? pl.bn / 2 : pl.bn) || a.K % 256) return hipErrorInvalidValue;
+  // folded T5LayerNorm: the normalised row must fit one norm record
+  if (epi == EPI_RESID && a.nx && (!a.rec || !a.ngamma || a.N != a.ldo || a.N > NORM_REC_MAX_D))
+    return hipErrorInvalidValue;
+  if (epi != EPI_RESID && a.rec && a.K > NORM_REC_MAX_D) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_F16: return launch_epi<EPI_F16>(wfmt, pl, a, s);
     case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, pl, a, s);

@@ -66,7 +66,7 @@ __device__ __forceinline__ float sq4(float4 v) { return v.x * v.x + v.y * v.y + 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       _Float16* __restrict__ out, int T, int D,
-                                                      float eps) {
+                                                      float eps, float* __restrict__ rec) {
   __shared__ float part[4][16];
   // gamma of the kept blocks, staged once per workgroup: the per-lane gamma reads come from
   // LDS instead of adding as many global loads as the x reads themselves
@@ -103,13 +103,39 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const float tot = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
   const float inv = 1.0f / sqrtf(tot / (float)D + eps);
   _Float16* ob = out + (size_t)blockIdx.x * nblk * 512 + lane * 8;
-  auto emit = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
+  auto emit_n = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
     h8 o = h8{(_Float16)((a.x * inv) * ga.x), (_Float16)((a.y * inv) * ga.y),
               (_Float16)((a.z * inv) * ga.z), (_Float16)((a.w * inv) * ga.w),
               (_Float16)((b.x * inv) * gb.x), (_Float16)((b.y * inv) * gb.y),
               (_Float16)((b.z * inv) * gb.z), (_Float16)((b.w * inv) * gb.w)};
     *reinterpret_cast<h8*>(ob + (size_t)kb * 512) = o;
   };
+  // Record mode (the batched GEMMs fold the norm, see GemmArgs::rec): the operand is
+  // f16(x * gamma * s) with the power of two s = norm_operand_scale(inv), and the token's
+  // record carries the whole sum of squares in slot 0 and s in slot 15, so the consuming
+  // GEMM recomputes this same inv and scales its result by inv / s.
+  const float sc = rec ? norm_operand_scale(inv) : 0.f;
+  auto emit_s = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
+    h8 o = h8{(_Float16)((a.x * ga.x) * sc), (_Float16)((a.y * ga.y) * sc),
+              (_Float16)((a.z * ga.z) * sc), (_Float16)((a.w * ga.w) * sc),
+              (_Float16)((b.x * gb.x) * sc), (_Float16)((b.y * gb.y) * sc),
+              (_Float16)((b.z * gb.z) * sc), (_Float16)((b.w * gb.w) * sc)};
+    *reinterpret_cast<h8*>(ob + (size_t)kb * 512) = o;
+  };
+  auto emit = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
+    if (rec)
+      emit_s(kb, a, b, ga, gb);
+    else
+      emit_n(kb, a, b, ga, gb);
+  };
+  if (rec && wave == 0 && lane < 16 && live) {
+    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    d[0] = make_float4(tot, 0.f, 0.f, 0.f);
+    d[1] = z;
+    d[2] = z;
+    d[3] = make_float4(0.f, 0.f, 0.f, sc);
+  }
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
     const int kb = wave + 4 * j;
@@ -187,9 +213,9 @@ hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, 
   return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
-                          hipStream_t s) {
+                          hipStream_t s, float* rec) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec);
   return hipGetLastError();
 }
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s) {

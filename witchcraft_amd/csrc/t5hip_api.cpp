@@ -93,6 +93,7 @@ struct t5h_model {
   bool batched_only = false;  // route every linear through the batched GEMM (t5h_ffn_block mode 1)
   int gemm_bn_override = 0;
   int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail
+  bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
 
   // ---- weights (one device arena) ----
   void* arena = nullptr;
@@ -116,6 +117,10 @@ struct t5h_model {
   int tpad = 0;
   float* x = nullptr;
   _Float16* xn = nullptr;
+  // Norm records of the folded T5LayerNorm (GemmArgs::rec), [tpad][16] f32 each: rec0 for the
+  // norm before attention and the final one, rec1 for the norm before the FFN.
+  float* rec0 = nullptr;
+  float* rec1 = nullptr;
   _Float16* qkvb = nullptr;
   _Float16* ao = nullptr;
   _Float16* hb = nullptr;
@@ -281,6 +286,7 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   const size_t o_ids = take((size_t)tpad * 4);
   const size_t o_cu = take((size_t)(capB + 1) * 4);
   const size_t o_work = take((size_t)capW * 8);
+  const size_t o_rec = take((size_t)2 * tpad * 16 * 4);
   if (m->ws) {
     HIP_OK(hipStreamSynchronize(m->stream));
     HIP_OK(hipFree(m->ws));
@@ -305,6 +311,9 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   m->ids = (uint32_t*)(base + o_ids);
   m->cu = (int*)(base + o_cu);
   m->work = (int2*)(base + o_work);
+  // zero-filled above: record slots past d_model / 64 must read as 0
+  m->rec0 = (float*)(base + o_rec);
+  m->rec1 = m->rec0 + (size_t)tpad * 16;
   m->cap_tokens = tpad - 128;
   m->cap_seqs = capB;
   m->cap_work = capW;
@@ -380,11 +389,27 @@ bool use_gemv(const t5h_model* m, int M) {
   return M <= t5k::GEMV_MAX_M && !m->gemm_mw_override && !m->batched_only;
 }
 
+// A T5LayerNorm folded into the batched GEMMs around it (GemmArgs::rec): a consumer passes
+// rec (and rec_next, where the next producer's operand scale goes); a residual producer
+// passes rec, nx (the operand buffer) and ngamma (the weight of the norm that follows).
+struct NormLink {
+  float* rec = nullptr;
+  float* rec_next = nullptr;
+  _Float16* nx = nullptr;
+  const float* ngamma = nullptr;
+};
+
+// True when this forward's batched GEMMs fold the norms (the row fits one norm record).
+bool fold_norm(const t5h_model* m, int T) {
+  const int D = m->cfg.d_model;
+  return !use_gemv(m, T) && !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
+}
+
 // C = A . W^T (+ epilogue).  norm_w: on the GEMV path the operand is T5LayerNorm(m->x) with
 // this weight, computed inside the kernel (A is then unused); callers pass it only when
-// use_gemv() holds.
+// use_gemv() holds.  nl: folded norm on the batched path (fold_norm() holds).
 int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, const _Float16* A, int lda,
-         int M, void* out, int ldo, int n_off = 0, const float* norm_w = nullptr) {
+         int M, void* out, int ldo, int n_off = 0, const float* norm_w = nullptr, const NormLink* nl = nullptr) {
   GemmArgs a{};
   a.A = A;
   a.lda = lda;
@@ -406,6 +431,7 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
   Timed t(m, kind, flops, bytes);
   if (use_gemv(m, M)) {
+    if (nl) return fail(T5H_ERR_INVALID, "internal: folded norm requested on the GEMV path");
     if (norm_w) {
       a.xf = m->x;
       a.gamma = norm_w;
@@ -415,6 +441,13 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
     return T5H_OK;
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
+  if (nl) {
+    a.rec = nl->rec;
+    a.rec_next = nl->rec_next;
+    a.nx = nl->nx;
+    a.ngamma = nl->ngamma;
+    a.eps = m->cfg.layer_norm_epsilon;
+  }
   const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
                                             m->gemm_bn_override, m->gemm_tail_override);
   HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
@@ -496,19 +529,53 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
   return nullptr;
 }
 
-int run_block(t5h_model* m, int l, int T, int nwork) {
+// T5LayerNorm of the residual stream in record mode, for GEMMs that fold the norm.
+int prenorm_rec(t5h_model* m, const float* w, int T) {
+  Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
+  const hipError_t e = t5k::launch_rmsnorm(m->x, w, m->xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
+                                           m->stream, m->rec0);
+  if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
+  return T5H_OK;
+}
+
+// One encoder block.  When the batched GEMMs fold the norms (fold_norm), the operand of the
+// block's first norm is either made here (operand_ready false) or was left in m->xn / rec0 by
+// the previous block's wo GEMM; with next_gamma set, this block's wo GEMM in turn prepares the
+// operand of the norm that follows (next block's first norm or the final one).
+int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
+              const float* next_gamma = nullptr) {
   const t5h_config& c = m->cfg;
   const Layer& Ly = m->layers[l];
   const int D = c.d_model, inner = m->inner;
+  const bool fold = fold_norm(m, T);
   int rc;
-  const float* nw0 = prenorm(m, Ly.ln0, T, rc);
-  if (rc) return rc;
-  if (Ly.fused_qkv) {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0))) return rc;
+  const float* nw0 = nullptr;
+  NormLink qn, on, fn, wn;  // QKV consumer, O producer, FFN consumer, wo producer
+  const NormLink* qkv_nl = nullptr;
+  if (fold) {
+    if (!operand_ready && (rc = prenorm_rec(m, Ly.ln0, T))) return rc;
+    qn.rec = m->rec0;
+    qn.rec_next = m->rec1;
+    on.rec = m->rec1;
+    on.nx = m->xn;
+    on.ngamma = Ly.ln1;
+    fn.rec = m->rec1;
+    fn.rec_next = m->rec0;
+    wn.rec = m->rec0;
+    wn.nx = m->xn;
+    wn.ngamma = next_gamma;
+    qkv_nl = &qn;
   } else {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner, nw0))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner, nw0))) return rc;
+    nw0 = prenorm(m, Ly.ln0, T, rc);
+    if (rc) return rc;
+  }
+  if (Ly.fused_qkv) {
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0, qkv_nl))) return rc;
+  } else {
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0, qkv_nl))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner, nw0, qkv_nl))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner, nw0, qkv_nl)))
+      return rc;
   }
   {
     AttnArgs a{};
@@ -523,15 +590,24 @@ int run_block(t5h_model* m, int l, int T, int nwork) {
     Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
   }
-  if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D))) return rc;
-  const float* nw1 = prenorm(m, Ly.ln1, T, rc);
-  if (rc) return rc;
-  if (c.feed_forward_gated) {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff, 0, nw1))) return rc;
-  } else {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff, 0, nw1))) return rc;
+  if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D, 0, nullptr, fold ? &on : nullptr)))
+    return rc;
+  const float* nw1 = nullptr;
+  if (!fold) {
+    nw1 = prenorm(m, Ly.ln1, T, rc);
+    if (rc) return rc;
   }
-  if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, D))) return rc;
+  const NormLink* ffn_nl = fold ? &fn : nullptr;
+  if (c.feed_forward_gated) {
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff, 0, nw1, ffn_nl)))
+      return rc;
+  } else {
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff, 0, nw1, ffn_nl)))
+      return rc;
+  }
+  if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, D, 0, nullptr,
+                 fold && next_gamma ? &wn : nullptr)))
+    return rc;
   return T5H_OK;
 }
 
@@ -547,11 +623,22 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
     HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag,
                              m->stream));
   }
-  for (int l = 0; l < c.num_layers; l++)
-    if ((rc = run_block(m, l, T, nwork))) return rc;
-  const float* nwf = prenorm(m, m->final_ln, T, rc);
-  if (rc) return rc;
-  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim, 0, nwf)))
+  const bool fold = fold_norm(m, T);
+  for (int l = 0; l < c.num_layers; l++) {
+    const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : m->final_ln;
+    if ((rc = run_block(m, l, T, nwork, l > 0, next))) return rc;
+  }
+  const float* nwf = nullptr;
+  NormLink pn;
+  if (fold) {
+    if (c.num_layers == 0 && (rc = prenorm_rec(m, m->final_ln, T))) return rc;
+    pn.rec = m->rec0;
+  } else {
+    nwf = prenorm(m, m->final_ln, T, rc);
+    if (rc) return rc;
+  }
+  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim, 0, nwf,
+                 fold ? &pn : nullptr)))
     return rc;
   {
     Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
@@ -640,6 +727,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     const int v = atoi(e);
     if (v >= 0 && v <= 2) m->gemm_tail_override = v;
   }
+  if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
   const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
 
   HostArena ha;

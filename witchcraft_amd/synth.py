@@ -69,12 +69,16 @@ def _normal(seed: int, name: str, shape, std: float) -> np.ndarray:
 
 
 def make_model(cfg: dict = XTR_BASE, seed: int = 0, layout: str = "q4k", emb_format: str = "f32",
-               norm_jitter: float = 0.1, bias_std: float | None = None) -> bytes:
+               norm_jitter: float = 0.1, bias_std: float | None = None,
+               std_over: dict | None = None) -> bytes:
     """Build a GGUF image of a random-init encoder.
 
     layout: "q4k" (every linear Q4_K) or "hybrid" (q/k/v/o/wo F32, wi_0/wi_1/linear Q4_K).
     emb_format: "f32" or "q4k" for the embedding table.
     norm_jitter: RMSNorm weights are 1 + jitter * N(0,1) (0 gives the all-ones init).
+    std_over: {name fragment: std} for the linears whose tensor name contains the fragment
+    (default std 0.02), e.g. {"DenseReluDense.wo": 20.0} for a residual stream that grows
+    by orders of magnitude in one FFN.
     """
     if layout not in ("q4k", "hybrid"):
         raise ValueError("layout must be 'q4k' or 'hybrid'")
@@ -86,6 +90,9 @@ def make_model(cfg: dict = XTR_BASE, seed: int = 0, layout: str = "q4k", emb_for
     ts: list[Tensor] = []
 
     def dense(name, rows, cols, quant: bool, std=0.02):
+        for frag, v in (std_over or {}).items():
+            if frag in name:
+                std = v
         w = _normal(seed, name, (rows, cols), std)
         if quant:
             ts.append(Tensor(name, GGML_Q4_K, (rows, cols), quantize_q4k(w).tobytes()))
