@@ -38,6 +38,86 @@ __device__ __forceinline__ int vslot(int key) {
   return (key & ~31) + 8 * ((kk >> 2) & 3) + 4 * (kk >> 4);
 }
 
+// One key tile of one wave's 16 queries: S^T = K . Q^T, bias, online softmax, O^T += V^T . P^T.
+// NKB = 16-key blocks of the tile that hold keys < L (the rest are skipped: their P is 0);
+// MASK: the tile holds keys >= L, which get score -inf (only a sequence's last tile).
+template <int NKB, bool MASK>
+__device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* Vtb, const float* Bsb, int bofs,
+                                          const h8 (&qf)[2], int k0, int L, float& m_run, float& l_run,
+                                          f4 (&o)[4]) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  // S^T[key][query] for the valid key blocks of 16
+  f4 s[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++) {
+    s[kb] = f4{0.f, 0.f, 0.f, 0.f};
+    if (kb >= NKB) continue;
+#pragma unroll
+    for (int ds = 0; ds < 2; ds++) {
+      const h8 a = *reinterpret_cast<const h8*>(&Ksb[(kb * 16 + lr) * KPAD + ds * 32 + lg * 8]);
+      s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
+    }
+  }
+  // bias, mask, running max
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      s[kb][i] += Bsb[bofs + kb * 16 + i];
+      if (MASK && k0 + kb * 16 + lg * 4 + i >= L) s[kb][i] = -INFINITY;
+      mx = fmaxf(mx, s[kb][i]);
+    }
+  mx = max_xor32(max_xor16(mx));
+  // The reference max moves only when a score exceeds it by more than RESCALE (or on the
+  // first tile, where m_run = -inf), so P <= e^RESCALE and the rescaling of O and l below
+  // is skipped for a whole wave on most tiles.  Same result up to rounding: P and l carry
+  // the same factor, divided out at the end.  mx is finite: key k0 < L is always valid.
+  const float m_new = mx > m_run + RESCALE ? mx : m_run;
+  // e^(v - m) = 2^(v log2e - m log2e): one FMA and one v_exp_f32 per score
+  const float mb = -m_new * LOG2E;
+  float rs = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], LOG2E, mb));
+      s[kb][i] = e;
+      rs += e;
+    }
+  rs = sum_xor32(sum_xor16(rs));
+  if (__any(m_new != m_run)) {
+    // exactly 1 for lanes whose max did not move (the wave-wide test also sees padding
+    // queries, which must not perturb real ones); 0 on the first tile (m_run = -inf)
+    const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
+    l_run *= corr;
+#pragma unroll
+    for (int db = 0; db < 4; db++) o[db] *= corr;
+  }
+  l_run += rs;
+  m_run = m_new;
+
+  // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; K-slots 8lg..8lg+7 of step ks are
+  // keys {32ks + 4lg + 0..3, 32ks + 16 + 4lg + 0..3} in both operands.  A step whose 32 keys
+  // are all past L adds nothing and is skipped.
+  constexpr int NKS = (NKB + 1) / 2;
+  h8 pb[2];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ks++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      pb[ks][i] = (_Float16)s[2 * ks][i];
+      pb[ks][4 + i] = (_Float16)s[2 * ks + 1][i];
+    }
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const h8 a = *reinterpret_cast<const h8*>(&Vtb[(db * 16 + lr) * VPAD + ks * 32 + lg * 8]);
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[ks], o[db], 0, 0, 0);
+    }
+}
+
 __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KT * KPAD];
   __shared__ __attribute__((aligned(16))) _Float16 Vt[2][DK * VPAD];
@@ -102,85 +182,27 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
   __syncthreads();
   // Bs index of this lane's (key 4lg + i of key block 0, query qi): (j - qi) - (k0 - q0 - 63)
   const int bofs = (QT - 1) - wave * 16 - lr + 4 * lg;
+  // Waves whose 16 queries all lie past L (in a sequence's last query tile) only help stage
+  // the tiles.  The test is wave-uniform.
+  const bool active = __builtin_amdgcn_readfirstlane(q0 + wave * 16) < L;
   for (int t = 0; t < ntile; ++t) {
     const int k0 = t * KT, buf = t & 1;
     if (t + 1 < ntile) gload(k0 + KT);
-
-    // S^T[key][query] for 4 key blocks of 16
-    f4 s[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
-      s[kb] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < 2; ds++) {
-        const h8 a = *reinterpret_cast<const h8*>(&Ks[buf][(kb * 16 + lr) * KPAD + ds * 32 + lg * 8]);
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
+    if (active) {
+      const _Float16* Ksb = Ks[buf];
+      const _Float16* Vtb = Vt[buf];
+      const float* Bsb = Bs[buf];
+      if (k0 + KT <= L) {
+        attn_tile<4, false>(Ksb, Vtb, Bsb, bofs, qf, k0, L, m_run, l_run, o);
+      } else {  // the last tile: only its key blocks below L
+        switch ((L - k0 + 15) >> 4) {
+          case 1: attn_tile<1, true>(Ksb, Vtb, Bsb, bofs, qf, k0, L, m_run, l_run, o); break;
+          case 2: attn_tile<2, true>(Ksb, Vtb, Bsb, bofs, qf, k0, L, m_run, l_run, o); break;
+          case 3: attn_tile<3, true>(Ksb, Vtb, Bsb, bofs, qf, k0, L, m_run, l_run, o); break;
+          default: attn_tile<4, true>(Ksb, Vtb, Bsb, bofs, qf, k0, L, m_run, l_run, o); break;
+        }
       }
     }
-    // bias, mask (only the last tile of a sequence has keys past L), running max
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) s[kb][i] += Bs[buf][bofs + kb * 16 + i];
-    if (k0 + KT > L) {
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (k0 + kb * 16 + lg * 4 + i >= L) s[kb][i] = -INFINITY;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kb][i]);
-    mx = max_xor32(max_xor16(mx));
-    // The reference max moves only when a score exceeds it by more than RESCALE (or on the
-    // first tile, where m_run = -inf), so P <= e^RESCALE and the rescaling of O and l below
-    // is skipped for a whole wave on most tiles.  Same result up to rounding: P and l carry
-    // the same factor, divided out at the end.  mx is finite: key k0 < L is always valid.
-    const float m_new = mx > m_run + RESCALE ? mx : m_run;
-    // e^(v - m) = 2^(v log2e - m log2e): one FMA and one v_exp_f32 per score
-    const float mb = -m_new * LOG2E;
-    float rs = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], LOG2E, mb));
-        s[kb][i] = e;
-        rs += e;
-      }
-    rs = sum_xor32(sum_xor16(rs));
-    if (__any(m_new != m_run)) {
-      // exactly 1 for lanes whose max did not move (the wave-wide test also sees padding
-      // queries, which must not perturb real ones); 0 on the first tile (m_run = -inf)
-      const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
-      l_run *= corr;
-#pragma unroll
-      for (int db = 0; db < 4; db++) o[db] *= corr;
-    }
-    l_run += rs;
-    m_run = m_new;
-
-    // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; K-slots 8lg..8lg+7 of step ks are
-    // keys {32ks + 4lg + 0..3, 32ks + 16 + 4lg + 0..3} in both operands.
-    h8 pb[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        pb[ks][i] = (_Float16)s[2 * ks][i];
-        pb[ks][4 + i] = (_Float16)s[2 * ks + 1][i];
-      }
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const h8 a = *reinterpret_cast<const h8*>(&Vt[buf][(db * 16 + lr) * VPAD + ks * 32 + lg * 8]);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[ks], o[db], 0, 0, 0);
-      }
-
     if (t + 1 < ntile) lstore(buf ^ 1);
     __syncthreads();
   }
