@@ -147,8 +147,11 @@ constexpr int GEMV_MAX_M = 64;
 hipError_t launch_gemv(int epi, int wfmt, const GemmArgs& a, hipStream_t s);
 void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
+// With rec set, also the first block's T5LayerNorm (weight gamma) in record mode into xn / rec,
+// as launch_rmsnorm's record mode (D <= 1024).
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
-                        float* x, unsigned* err_flag, hipStream_t s);
+                        float* x, unsigned* err_flag, hipStream_t s, const float* gamma = nullptr,
+                        float eps = 0.f, _Float16* xn = nullptr, float* rec = nullptr);
 // rec: when set, record mode for a consuming GEMM that folds the norm (GemmArgs::rec).
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
                           hipStream_t s, float* rec = nullptr);

@@ -13,43 +13,109 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Embedding gather (candle quantized_nn::Embedding, src/quantized_t5.rs:659,687):
 // x[t] = table[ids[t]].  The table is f32 or Q4_K (dequantized on the fly, bit-exact).
 // One wave per token.  Ids outside the vocabulary yield a zero row and set *err.
+// With rec set (D <= EMB_NORM_MAX_D) the wave also emits the first block's T5LayerNorm in
+// record mode, as rmsnorm_kernel does: the operand f16(x * gamma * s) and the token's record
+// (whole sum of squares in slot 0, s in slot 15) for a GEMM that folds the norm.
+constexpr int EMB_NORM_MAX_D = 1024;
+
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ ids, int T,
                                                     const void* __restrict__ table, int fmt, int vocab,
-                                                    int D, float* __restrict__ x, unsigned* err) {
+                                                    int D, float* __restrict__ x, unsigned* err,
+                                                    const float* __restrict__ gamma, float eps,
+                                                    _Float16* __restrict__ xn, float* __restrict__ rec) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int lane = threadIdx.x & 63;
   const uint32_t id = ids[t];
   float* xr = x + (size_t)t * D;
-  if (id >= (uint32_t)vocab) {
-    for (int i = lane; i < D; i += 64) xr[i] = 0.f;
-    if (lane == 0) *(volatile unsigned*)err = 1u;  // host-mapped flag; every writer stores 1
+  const bool bad = id >= (uint32_t)vocab;
+  if (bad && lane == 0) *(volatile unsigned*)err = 1u;  // host-mapped flag; every writer stores 1
+  if (fmt == EMB_F32 || bad) {
+    // lane holds columns 4i .. 4i+3, i = lane + 64j
+    const float4* src = reinterpret_cast<const float4*>((const float*)table + (size_t)(bad ? 0 : id) * D);
+    float4 v[EMB_NORM_MAX_D / 256];
+    float ss = 0.f;
+    if (rec) {
+#pragma unroll
+      for (int j = 0; j < EMB_NORM_MAX_D / 256; j++) {
+        const int i = lane + 64 * j;
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < D / 4 && !bad) v[j] = src[i];
+        if (i < D / 4) reinterpret_cast<float4*>(xr)[i] = v[j];
+        ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+      }
+      const float tot = wave_sum(ss);
+      const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+      const float sc = norm_operand_scale(inv);
+#pragma unroll
+      for (int j = 0; j < EMB_NORM_MAX_D / 256; j++) {
+        const int i = lane + 64 * j;
+        if (i >= D / 4) continue;
+        const float4 g = reinterpret_cast<const float4*>(gamma)[i];
+        *reinterpret_cast<h4*>(xn + tiled_index(t, 4 * i, D)) =
+            h4{(_Float16)((v[j].x * g.x) * sc), (_Float16)((v[j].y * g.y) * sc), (_Float16)((v[j].z * g.z) * sc),
+               (_Float16)((v[j].w * g.w) * sc)};
+      }
+      if (lane < 4) {
+        float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16) + lane;
+        *d = lane == 0 ? make_float4(tot, 0.f, 0.f, 0.f)
+                       : (lane == 3 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
+      }
+      return;
+    }
+    for (int i = lane; i < D / 4; i += 64)
+      reinterpret_cast<float4*>(xr)[i] = bad ? make_float4(0.f, 0.f, 0.f, 0.f) : src[i];
     return;
   }
-  if (fmt == EMB_F32) {
-    const float4* src = reinterpret_cast<const float4*>((const float*)table + (size_t)id * D);
-    for (int i = lane; i < D / 4; i += 64) reinterpret_cast<float4*>(xr)[i] = src[i];
-  } else {  // Q4_K table: D/256 blocks per row
-    const uint8_t* row = (const uint8_t*)table + (size_t)id * (D / QK_K) * Q4K_BYTES;
-    for (int e = lane; e < D; e += 64) {
-      const uint8_t* b = row + (e / QK_K) * Q4K_BYTES;
-      const int k = e % QK_K, c = k / 64, w = k % 64, hi = w >= 32, l = w & 31;
-      const int j = 2 * c + hi;
-      const uint8_t* s = b + 4;
-      int sc, m;
-      if (j < 4) {
-        sc = s[j] & 63;
-        m = s[j + 4] & 63;
-      } else {
-        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-      }
-      const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
-      const float dmin = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
-      const uint8_t q = b[16 + 32 * c + l];
-      const float ds = d * (float)sc, mm = dmin * (float)m;
-      xr[e] = ds * (float)(hi ? (q >> 4) : (q & 15)) - mm;
+  // Q4_K table: D/256 blocks per row
+  const uint8_t* row = (const uint8_t*)table + (size_t)id * (D / QK_K) * Q4K_BYTES;
+  auto deq = [&](int e) {
+    const uint8_t* b = row + (e / QK_K) * Q4K_BYTES;
+    const int k = e % QK_K, c = k / 64, w = k % 64, hi = w >= 32, l = w & 31;
+    const int jj = 2 * c + hi;
+    const uint8_t* sb = b + 4;
+    int sc, m;
+    if (jj < 4) {
+      sc = sb[jj] & 63;
+      m = sb[jj + 4] & 63;
+    } else {
+      sc = (sb[jj + 4] & 15) | ((sb[jj - 4] >> 6) << 4);
+      m = (sb[jj + 4] >> 4) | ((sb[jj] >> 6) << 4);
     }
+    const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    const float dmin = f16_bits_to_f32((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+    const uint8_t q = b[16 + 32 * c + l];
+    const float ds = d * (float)sc, mm = dmin * (float)m;
+    return ds * (float)(hi ? (q >> 4) : (q & 15)) - mm;
+  };
+  if (!rec) {
+    for (int e = lane; e < D; e += 64) xr[e] = deq(e);
+    return;
+  }
+  // lane holds columns lane + 64j
+  float v[EMB_NORM_MAX_D / 64];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < EMB_NORM_MAX_D / 64; j++) {
+    const int e = lane + 64 * j;
+    v[j] = 0.f;
+    if (e >= D) continue;
+    v[j] = deq(e);
+    xr[e] = v[j];
+    ss += v[j] * v[j];
+  }
+  const float tot = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+  const float sc = norm_operand_scale(inv);
+#pragma unroll
+  for (int j = 0; j < EMB_NORM_MAX_D / 64; j++) {
+    const int e = lane + 64 * j;
+    if (e < D) xn[tiled_index(t, e, D)] = (_Float16)((v[j] * gamma[e]) * sc);
+  }
+  if (lane < 4) {
+    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16) + lane;
+    *d = lane == 0 ? make_float4(tot, 0.f, 0.f, 0.f)
+                   : (lane == 3 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
   }
 }
 
@@ -207,9 +273,12 @@ __global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict
 
 namespace t5k {
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
-                        float* x, unsigned* err, hipStream_t s) {
+                        float* x, unsigned* err, hipStream_t s, const float* gamma, float eps, _Float16* xn,
+                        float* rec) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err);
+  if (rec && (D > EMB_NORM_MAX_D || D % 32 || !gamma || !xn)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err,
+                     gamma, eps, xn, rec);
   return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,

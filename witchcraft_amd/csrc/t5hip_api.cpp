@@ -618,20 +618,21 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
   if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
   if ((rc = upload_batch(m, cu, B, nwork))) return rc;
   const t5h_config& c = m->cfg;
+  // With folded norms the embedding gather also emits the first norm's operand and records.
+  const bool fold = fold_norm(m, T);
   {
     Timed t(m, K_EMBED, 0, (double)T * c.d_model * 8);
-    HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag,
-                             m->stream));
+    const float* g0 = c.num_layers > 0 ? m->layers[0].ln0 : m->final_ln;
+    HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag, m->stream,
+                             g0, c.layer_norm_epsilon, fold ? m->xn : nullptr, fold ? m->rec0 : nullptr));
   }
-  const bool fold = fold_norm(m, T);
   for (int l = 0; l < c.num_layers; l++) {
     const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : m->final_ln;
-    if ((rc = run_block(m, l, T, nwork, l > 0, next))) return rc;
+    if ((rc = run_block(m, l, T, nwork, fold, next))) return rc;
   }
   const float* nwf = nullptr;
   NormLink pn;
   if (fold) {
-    if (c.num_layers == 0 && (rc = prenorm_rec(m, m->final_ln, T))) return rc;
     pn.rec = m->rec0;
   } else {
     nwf = prenorm(m, m->final_ln, T, rc);
