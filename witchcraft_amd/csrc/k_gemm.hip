@@ -524,7 +524,7 @@ static double thin_tile_cost(int bn, int mb) {
 // round that is mostly empty costs as much as a full one.  Every split at a multiple of the
 // full tile height and both thin heights is evaluated with list_makespan.
 // tail_override: -1 = choose, 0 = full tiles only, 1 / 2 = thin tiles of that height for the
-// last row of full tiles (tests).
+// last row of full tiles, 3 / 4 = thin tiles of height 1 / 2 for every row (tests, tuning).
 GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override) {
   GemmPlan pl;
   gemm_pick_tile(M, n_rows, cus, pl.mw, pl.bn);
@@ -534,9 +534,9 @@ GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override,
   pl.tail_mb = 0;
   if (pl.mw != 4 || M <= 0 || tail_override == 0) return pl;
   const int bm = 256, tiles_n = n_rows / pl.bn, full = (M + bm - 1) / bm;
-  if (tail_override == 1 || tail_override == 2) {
-    pl.tail_mb = tail_override;
-    pl.m_main = (full - 1) * bm;
+  if (tail_override >= 1 && tail_override <= 4) {  // 3, 4: every row in thin tiles of height 1, 2
+    pl.tail_mb = tail_override > 2 ? tail_override - 2 : tail_override;
+    pl.m_main = tail_override > 2 ? 0 : (full - 1) * bm;
     return pl;
   }
   double best = list_makespan(full * tiles_n, 0, 1.0, cus);

@@ -92,7 +92,7 @@ struct t5h_model {
   int gemm_mw_override = 0;  // T5H_GEMM_MW / T5H_GEMM_BN tuning knobs (0 = heuristic)
   bool batched_only = false;  // route every linear through the batched GEMM (t5h_ffn_block mode 1)
   int gemm_bn_override = 0;
-  int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail
+  int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail, 3 / 4 = all thin
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
 
   // ---- weights (one device arena) ----
@@ -726,7 +726,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   }
   if (const char* e = getenv("T5H_GEMM_TAIL")) {
     const int v = atoi(e);
-    if (v >= 0 && v <= 2) m->gemm_tail_override = v;
+    if (v >= 0 && v <= 4) m->gemm_tail_override = v;
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
   const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
