@@ -54,7 +54,7 @@ struct GemmArgs {
   float eps;
   // Batched GEMM only: T5LayerNorm folded into the GEMMs on either side of it.  Each token
   // has a 64-byte record rec[16m .. 16m+15]: slots t < 15 hold sums of x^2 over the columns
-  // [64t, 64t + 64) (slots past D/64 stay zero), slot 15 the power of two s with which the
+  // [64t, 64t + 64) (slots past D/64 are ignored), slot 15 the power of two s with which the
   // f16 operand of that token was stored.
   //  * producer (EPI_RESID with nx set): x += acc as usual; then nx = f16(x * ngamma * s) in
   //    operand order with s = rec[16m + 15], and each tile's sums of x^2 into rec.
@@ -69,6 +69,10 @@ struct GemmArgs {
 
 // Largest row length (d_model) whose sums of squares fit a norm record (15 slots of 64).
 constexpr int NORM_REC_MAX_D = 15 * 64;
+// The GEMV kernels (M <= GEMV_MAX_M) fold the norm the same way with 64-float records: a
+// GEMV workgroup owns 16 columns, so slot t < 63 holds the sum of x^2 over [16t, 16t + 16)
+// and slot 63 the operand scale s.
+constexpr int NORM_REC_GEMV = 64;
 
 // The operand scale that follows an inverse RMS: the power of two at or below inv, / 16.
 // Stored values then have an RMS near |gamma| / 16, leaving room for the residual stream to
@@ -148,13 +152,13 @@ hipError_t launch_gemv(int epi, int wfmt, const GemmArgs& a, hipStream_t s);
 void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn);
 hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t s);
 // With rec set, also the first block's T5LayerNorm (weight gamma) in record mode into xn / rec,
-// as launch_rmsnorm's record mode (D <= 1024).
+// as launch_rmsnorm's record mode (D <= 1024); rec_stride 16 (batched GEMMs) or 64 (GEMV).
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
                         float* x, unsigned* err_flag, hipStream_t s, const float* gamma = nullptr,
-                        float eps = 0.f, _Float16* xn = nullptr, float* rec = nullptr);
+                        float eps = 0.f, _Float16* xn = nullptr, float* rec = nullptr, int rec_stride = 16);
 // rec: when set, record mode for a consuming GEMM that folds the norm (GemmArgs::rec).
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
-                          hipStream_t s, float* rec = nullptr);
+                          hipStream_t s, float* rec = nullptr, int rec_stride = 16);
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s);
 // Query-side scoring: C = A . B^T (f32) and its per-row argmax (k_score.hip).

@@ -254,9 +254,18 @@ __device__ __forceinline__ void norm_rec_load(const GemmArgs& p, int mrow0, floa
 }
 template <int MB>
 __device__ __forceinline__ float norm_factor(const GemmArgs& p, int mrow0, int n0, const float4 (&r)[4]) {
-  const float4 a = r[0], b = r[1], c = r[2], d = r[3];
-  const float tot = (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) +
-                    (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + d.z));
+  // slots past K / 64 are masked: the record array may hold another layout's data there
+  const int ns = p.K / 64;
+  float v[15];
+#pragma unroll
+  for (int i = 0; i < 15; i++) {
+    const float4 q = r[i / 4];
+    const float x = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+    v[i] = i < ns ? x : 0.f;
+  }
+  const float tot = (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) +
+                    (((v[8] + v[9]) + (v[10] + v[11])) + ((v[12] + v[13]) + v[14]));
+  const float4 d = r[3];
   const float inv = 1.0f / sqrtf(tot / (float)p.K + p.eps);
   const int m = norm_row<MB>(mrow0);
   if (p.rec_next && n0 == 0 && (threadIdx.x & 63) < 16 * MB && m < p.M)

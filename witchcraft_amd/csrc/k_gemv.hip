@@ -18,6 +18,10 @@
 //    1/rms from the f32 residual stream and the operand is built as f16((x * inv) * gamma)
 //    while loading -- the standalone RMSNorm launch and its round trip disappear.
 //  * The residual epilogue fetches its x quad at kernel start.
+//  * Folded T5LayerNorm (GemmArgs::rec, 64-float records): the residual GEMV stores the next
+//    norm's operand f16(x * gamma * s) and its 16 columns' sum of x^2; the GEMV that consumes
+//    it loads the f16 operand like any other and scales its sums by rsqrt(mean(x^2) + eps) / s
+//    in the epilogue, so nothing waits on the norm before the dot products start.
 #include "common.hpp"
 #include "epilogue.hpp"
 #include "q4k.hpp"
@@ -227,6 +231,25 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
 #undef GEMV_LOAD_W
 #undef GEMV_LOAD_X
 
+  // Folded T5LayerNorm (GemmArgs::rec, 64-float records): the epilogue wave of token block
+  // mt = wave fetches its token's record while the partial sums meet in LDS -- as a consumer
+  // the 63 partial sums (lane group lg holds slots 16lg .. 16lg + 15) and the operand scale,
+  // as a producer that scale and gamma.  (Fetched before the K loop they would stay live
+  // through it and spill at the 1024-thread register budget.)
+  float4 nrec[4];
+  float nsc = 1.f;
+  float4 ngam = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (p.rec && wave < MT) {
+    const float* r = p.rec + (size_t)((tb0 + wave) * 16 + lr) * NORM_REC_GEMV;
+    nsc = r[NORM_REC_GEMV - 1];
+    if constexpr (EPI == EPI_RESID) {
+      ngam = *reinterpret_cast<const float4*>(p.ngamma + n0 + 4 * lg);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) nrec[i] = reinterpret_cast<const float4*>(r + 16 * lg)[i];
+    }
+  }
+
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
@@ -242,15 +265,62 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
       for (int w = 1; w < nw; w++) v[g] += red[((w * G + g) * MT + mt) * 64 + lane];
     }
     const int m = (tb0 + mt) * 16 + lr;
-    if (m >= p.M) continue;
-    if constexpr (EPI == EPI_GATED) {
-      store_quad_gated(p, m, n0 + 4 * lg, v[0], v[G - 1]);
-    } else if constexpr (EPI == EPI_RESID) {  // x quad prefetched above for mt == wave
+    const bool live = m < p.M;
+    const float* rrow = p.rec ? p.rec + (size_t)m * NORM_REC_GEMV : nullptr;
+    if constexpr (EPI == EPI_RESID) {  // x quad prefetched above for mt == wave
       float4* xp = reinterpret_cast<float4*>((float*)p.out + (size_t)m * p.ldo + n0 + 4 * lg);
-      const float4 r = mt == wave ? xres : *xp;
-      *xp = make_float4(r.x + v[0][0], r.y + v[0][1], r.z + v[0][2], r.w + v[0][3]);
+      float4 r = mt == wave ? xres : (live ? *xp : make_float4(0.f, 0.f, 0.f, 0.f));
+      r = make_float4(r.x + v[0][0], r.y + v[0][1], r.z + v[0][2], r.w + v[0][3]);
+      if (live) *xp = r;
+      if (p.nx) {  // next norm: f16(x * gamma * s) and the sum of x^2 over these 16 columns
+        const float sc = mt == wave ? nsc : rrow[NORM_REC_GEMV - 1];
+        const float4 g = mt == wave ? ngam : *reinterpret_cast<const float4*>(p.ngamma + n0 + 4 * lg);
+        const float ss = sum_xor32(sum_xor16((r.x * r.x + r.y * r.y) + (r.z * r.z + r.w * r.w)));
+        if (live) {
+          *reinterpret_cast<h4*>(p.nx + tiled_index(m, n0 + 4 * lg, p.ldo)) =
+              h4{(_Float16)((r.x * g.x) * sc), (_Float16)((r.y * g.y) * sc), (_Float16)((r.z * g.z) * sc),
+                 (_Float16)((r.w * g.w) * sc)};
+          if (lg == 0) p.rec[(size_t)m * NORM_REC_GEMV + n0 / 16] = ss;
+        }
+      }
+      continue;
     } else {
-      store_quad<EPI>(p, m, n0 + 4 * lg, v[0]);
+      if (p.rec) {  // folded norm: scale by rsqrt(mean(x^2) + eps) / s
+        float4 q[4];
+        float sc;
+        if (mt == wave) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) q[i] = nrec[i];
+          sc = nsc;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++) q[i] = reinterpret_cast<const float4*>(rrow + 16 * lg)[i];
+          sc = rrow[NORM_REC_GEMV - 1];
+        }
+        // slots 16lg + 4i + j; those past K / 16 (and slot 63, the scale) are masked: the
+        // record array may hold another layout's data there
+        const int ns = p.K / 16;
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int t = 16 * lg + 4 * i;
+          part += ((t < ns ? q[i].x : 0.f) + (t + 1 < ns ? q[i].y : 0.f)) +
+                  ((t + 2 < ns ? q[i].z : 0.f) + (t + 3 < ns ? q[i].w : 0.f));
+        }
+        const float tot = sum_xor32(sum_xor16(part));
+        const float inv = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+        const float f = inv / sc;
+#pragma unroll
+        for (int g = 0; g < G; g++) v[g] *= f;
+        if (p.rec_next && blockIdx.x == 0 && lg == 0 && live)
+          p.rec_next[(size_t)m * NORM_REC_GEMV + NORM_REC_GEMV - 1] = norm_operand_scale(inv);
+      }
+      if (!live) continue;
+      if constexpr (EPI == EPI_GATED) {
+        store_quad_gated(p, m, n0 + 4 * lg, v[0], v[G - 1]);
+      } else {
+        store_quad<EPI>(p, m, n0 + 4 * lg, v[0]);
+      }
     }
   }
 }
@@ -307,6 +377,11 @@ namespace t5k {
 hipError_t launch_gemv(int epi, int wfmt, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.M > GEMV_MAX_M || a.N % 16 || a.K % 256 || (a.xf && !a.gamma)) return hipErrorInvalidValue;
+  // folded T5LayerNorm: the row must fit one 64-float record
+  if (a.rec && a.xf) return hipErrorInvalidValue;
+  if (epi == EPI_RESID && a.nx && (!a.rec || !a.ngamma || a.N != a.ldo || a.N > 16 * (NORM_REC_GEMV - 1)))
+    return hipErrorInvalidValue;
+  if (epi != EPI_RESID && a.rec && a.K > 16 * (NORM_REC_GEMV - 1)) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_F16: return launch_epi<EPI_F16>(wfmt, a, s);
     case EPI_RESID: return launch_epi<EPI_RESID>(wfmt, a, s);

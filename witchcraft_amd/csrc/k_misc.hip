@@ -14,15 +14,16 @@ __device__ __forceinline__ float wave_sum(float v) {
 // x[t] = table[ids[t]].  The table is f32 or Q4_K (dequantized on the fly, bit-exact).
 // One wave per token.  Ids outside the vocabulary yield a zero row and set *err.
 // With rec set (D <= EMB_NORM_MAX_D) the wave also emits the first block's T5LayerNorm in
-// record mode, as rmsnorm_kernel does: the operand f16(x * gamma * s) and the token's record
-// (whole sum of squares in slot 0, s in slot 15) for a GEMM that folds the norm.
+// record mode, as rmsnorm_kernel does: the operand f16(x * gamma * s) and the token's record of
+// rs floats (whole sum of squares in slot 0, s in slot rs - 1) for a GEMM that folds the norm.
 constexpr int EMB_NORM_MAX_D = 1024;
 
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ ids, int T,
                                                     const void* __restrict__ table, int fmt, int vocab,
                                                     int D, float* __restrict__ x, unsigned* err,
                                                     const float* __restrict__ gamma, float eps,
-                                                    _Float16* __restrict__ xn, float* __restrict__ rec) {
+                                                    _Float16* __restrict__ xn, float* __restrict__ rec,
+                                                    int rs) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int lane = threadIdx.x & 63;
@@ -56,10 +57,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
             h4{(_Float16)((v[j].x * g.x) * sc), (_Float16)((v[j].y * g.y) * sc), (_Float16)((v[j].z * g.z) * sc),
                (_Float16)((v[j].w * g.w) * sc)};
       }
-      if (lane < 4) {
-        float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16) + lane;
+      if (lane < rs / 4) {
+        float4* d = reinterpret_cast<float4*>(rec + (size_t)t * rs) + lane;
         *d = lane == 0 ? make_float4(tot, 0.f, 0.f, 0.f)
-                       : (lane == 3 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
+                       : (lane == rs / 4 - 1 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
       }
       return;
     }
@@ -112,10 +113,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
     const int e = lane + 64 * j;
     if (e < D) xn[tiled_index(t, e, D)] = (_Float16)((v[j] * gamma[e]) * sc);
   }
-  if (lane < 4) {
-    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16) + lane;
+  if (lane < rs / 4) {
+    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * rs) + lane;
     *d = lane == 0 ? make_float4(tot, 0.f, 0.f, 0.f)
-                   : (lane == 3 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
+                   : (lane == rs / 4 - 1 ? make_float4(0.f, 0.f, 0.f, sc) : make_float4(0.f, 0.f, 0.f, 0.f));
   }
 }
 
@@ -132,7 +133,7 @@ __device__ __forceinline__ float sq4(float4 v) { return v.x * v.x + v.y * v.y + 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       _Float16* __restrict__ out, int T, int D,
-                                                      float eps, float* __restrict__ rec) {
+                                                      float eps, float* __restrict__ rec, int rs) {
   __shared__ float part[4][16];
   // gamma of the kept blocks, staged once per workgroup: the per-lane gamma reads come from
   // LDS instead of adding as many global loads as the x reads themselves
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   };
   // Record mode (the batched GEMMs fold the norm, see GemmArgs::rec): the operand is
   // f16(x * gamma * s) with the power of two s = norm_operand_scale(inv), and the token's
-  // record carries the whole sum of squares in slot 0 and s in slot 15, so the consuming
+  // record of rs floats carries the whole sum of squares in slot 0 and s in its last slot, so the consuming
   // GEMM recomputes this same inv and scales its result by inv / s.
   const float sc = rec ? norm_operand_scale(inv) : 0.f;
   auto emit_s = [&](int kb, float4 a, float4 b, float4 ga, float4 gb) {
@@ -195,12 +196,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       emit_n(kb, a, b, ga, gb);
   };
   if (rec && wave == 0 && lane < 16 && live) {
-    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * 16);
+    float4* d = reinterpret_cast<float4*>(rec + (size_t)t * rs);
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     d[0] = make_float4(tot, 0.f, 0.f, 0.f);
-    d[1] = z;
-    d[2] = z;
-    d[3] = make_float4(0.f, 0.f, 0.f, sc);
+    for (int i = 1; i < rs / 4 - 1; i++) d[i] = z;
+    d[rs / 4 - 1] = make_float4(0.f, 0.f, 0.f, sc);
   }
 #pragma unroll
   for (int j = 0; j < RN_KEEP; ++j) {
@@ -274,17 +274,19 @@ __global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict
 namespace t5k {
 hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, int vocab, int D,
                         float* x, unsigned* err, hipStream_t s, const float* gamma, float eps, _Float16* xn,
-                        float* rec) {
+                        float* rec, int rec_stride) {
   if (T <= 0) return hipSuccess;
-  if (rec && (D > EMB_NORM_MAX_D || D % 32 || !gamma || !xn)) return hipErrorInvalidValue;
+  if (rec && (D > EMB_NORM_MAX_D || D % 32 || !gamma || !xn || (rec_stride != 16 && rec_stride != 64)))
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err,
-                     gamma, eps, xn, rec);
+                     gamma, eps, xn, rec, rec_stride);
   return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
-                          hipStream_t s, float* rec) {
+                          hipStream_t s, float* rec, int rec_stride) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec);
+  if (rec && rec_stride != 16 && rec_stride != 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec, rec_stride);
   return hipGetLastError();
 }
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s) {

@@ -117,8 +117,9 @@ struct t5h_model {
   int tpad = 0;
   float* x = nullptr;
   _Float16* xn = nullptr;
-  // Norm records of the folded T5LayerNorm (GemmArgs::rec), [tpad][16] f32 each: rec0 for the
-  // norm before attention and the final one, rec1 for the norm before the FFN.
+  // Norm records of the folded T5LayerNorm (GemmArgs::rec), [tpad][16] f32 each on the batched
+  // path and [tpad][64] on the GEMV path: rec0 for the norm before attention and the final
+  // one, rec1 for the norm before the FFN.
   float* rec0 = nullptr;
   float* rec1 = nullptr;
   _Float16* qkvb = nullptr;
@@ -286,7 +287,7 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   const size_t o_ids = take((size_t)tpad * 4);
   const size_t o_cu = take((size_t)(capB + 1) * 4);
   const size_t o_work = take((size_t)capW * 8);
-  const size_t o_rec = take((size_t)2 * tpad * 16 * 4);
+  const size_t o_rec = take((size_t)2 * tpad * NORM_REC_GEMV * 4);
   if (m->ws) {
     HIP_OK(hipStreamSynchronize(m->stream));
     HIP_OK(hipFree(m->ws));
@@ -311,9 +312,8 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   m->ids = (uint32_t*)(base + o_ids);
   m->cu = (int*)(base + o_cu);
   m->work = (int2*)(base + o_work);
-  // zero-filled above: record slots past d_model / 64 must read as 0
   m->rec0 = (float*)(base + o_rec);
-  m->rec1 = m->rec0 + (size_t)tpad * 16;
+  m->rec1 = m->rec0 + (size_t)tpad * NORM_REC_GEMV;
   m->cap_tokens = tpad - 128;
   m->cap_seqs = capB;
   m->cap_work = capW;
@@ -399,15 +399,18 @@ struct NormLink {
   const float* ngamma = nullptr;
 };
 
-// True when this forward's batched GEMMs fold the norms (the row fits one norm record).
+// True when this forward's GEMMs fold the norms (the row fits one norm record).
 bool fold_norm(const t5h_model* m, int T) {
+  (void)T;
   const int D = m->cfg.d_model;
-  return !use_gemv(m, T) && !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
+  return !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
 }
+// Floats per norm record: the GEMV kernels keep one partial sum per 16 columns.
+int rec_stride(const t5h_model* m, int T) { return use_gemv(m, T) ? NORM_REC_GEMV : 16; }
 
 // C = A . W^T (+ epilogue).  norm_w: on the GEMV path the operand is T5LayerNorm(m->x) with
 // this weight, computed inside the kernel (A is then unused); callers pass it only when
-// use_gemv() holds.  nl: folded norm on the batched path (fold_norm() holds).
+// use_gemv() holds.  nl: folded norm (fold_norm() holds), on either path.
 int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, const _Float16* A, int lda,
          int M, void* out, int ldo, int n_off = 0, const float* norm_w = nullptr, const NormLink* nl = nullptr) {
   GemmArgs a{};
@@ -430,8 +433,15 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
                            (epi == EPI_RESID ? 2.0 : 1.0);
   const double bytes = W.bytes() * mats + 2.0 * M * W.K + out_bytes;
   Timed t(m, kind, flops, bytes);
+  if (nl) {
+    if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused and folded norm requested together");
+    a.rec = nl->rec;
+    a.rec_next = nl->rec_next;
+    a.nx = nl->nx;
+    a.ngamma = nl->ngamma;
+    a.eps = m->cfg.layer_norm_epsilon;
+  }
   if (use_gemv(m, M)) {
-    if (nl) return fail(T5H_ERR_INVALID, "internal: folded norm requested on the GEMV path");
     if (norm_w) {
       a.xf = m->x;
       a.gamma = norm_w;
@@ -441,13 +451,6 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
     return T5H_OK;
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
-  if (nl) {
-    a.rec = nl->rec;
-    a.rec_next = nl->rec_next;
-    a.nx = nl->nx;
-    a.ngamma = nl->ngamma;
-    a.eps = m->cfg.layer_norm_epsilon;
-  }
   const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
                                             m->gemm_bn_override, m->gemm_tail_override);
   HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
@@ -533,12 +536,12 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
 int prenorm_rec(t5h_model* m, const float* w, int T) {
   Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
   const hipError_t e = t5k::launch_rmsnorm(m->x, w, m->xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
-                                           m->stream, m->rec0);
+                                           m->stream, m->rec0, rec_stride(m, T));
   if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
   return T5H_OK;
 }
 
-// One encoder block.  When the batched GEMMs fold the norms (fold_norm), the operand of the
+// One encoder block.  When the GEMMs fold the norms (fold_norm), the operand of the
 // block's first norm is either made here (operand_ready false) or was left in m->xn / rec0 by
 // the previous block's wo GEMM; with next_gamma set, this block's wo GEMM in turn prepares the
 // operand of the norm that follows (next block's first norm or the final one).
@@ -624,7 +627,8 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
     Timed t(m, K_EMBED, 0, (double)T * c.d_model * 8);
     const float* g0 = c.num_layers > 0 ? m->layers[0].ln0 : m->final_ln;
     HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag, m->stream,
-                             g0, c.layer_norm_epsilon, fold ? m->xn : nullptr, fold ? m->rec0 : nullptr));
+                             g0, c.layer_norm_epsilon, fold ? m->xn : nullptr, fold ? m->rec0 : nullptr,
+                             rec_stride(m, T)));
   }
   for (int l = 0; l < c.num_layers; l++) {
     const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : m->final_ln;
