@@ -91,8 +91,7 @@ __host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]
   _Float16* out;        // [T][H*dkv] in operand order (tiled_index)
-  const int* cu;        // [B+1] device
-  const int2* work;     // (seq, q_tile) pairs
+  const int4* work;     // (sequence start, length, first query, 0) per 64-query tile
   const float* lut;     // [H][2*lutw+1] relative bias by (j - i), centred at lutw
   int heads, tpad, lutw;
 };

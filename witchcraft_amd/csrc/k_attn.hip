@@ -124,9 +124,8 @@ __global__ __launch_bounds__(256) void attn_relbias_kernel(AttnArgs p) {
   __shared__ float Bs[2][2 * KT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int2 wk = p.work[blockIdx.x / p.heads];
-  const int seq = wk.x, q0 = wk.y * QT, h = blockIdx.x % p.heads;
-  const int s0 = p.cu[seq], L = p.cu[seq + 1] - s0;
+  const int4 wk = p.work[blockIdx.x / p.heads];
+  const int s0 = wk.x, L = wk.y, q0 = wk.z, h = blockIdx.x % p.heads;
   const int lr = lane & 15, lg = lane >> 4;
 
   const size_t head_stride = (size_t)p.tpad * DK;

@@ -128,8 +128,7 @@ struct t5h_model {
   float* out = nullptr;
   float* norm = nullptr;
   uint32_t* ids = nullptr;
-  int* cu = nullptr;
-  int2* work = nullptr;
+  int4* work = nullptr;
   // Out-of-vocabulary flag in mapped pinned host memory: the embed kernel stores 1 through
   // err_flag (its device address); the host reads err_host after the stream is synchronised.
   unsigned* err_host = nullptr;
@@ -285,13 +284,12 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   const size_t o_out = take((size_t)tpad * c.proj_dim * 4);
   const size_t o_norm = take((size_t)tpad * 4);
   const size_t o_ids = take((size_t)tpad * 4);
-  const size_t o_cu = take((size_t)(capB + 1) * 4);
-  const size_t o_work = take((size_t)capW * 8);
+  const size_t o_work = take((size_t)capW * sizeof(int4));
   const size_t o_rec = take((size_t)2 * tpad * NORM_REC_GEMV * 4);
   if (m->ws) {
     HIP_OK(hipStreamSynchronize(m->stream));
     HIP_OK(hipFree(m->ws));
-    m->last_B = -1;  // device cu_seqlens / work list are gone
+    m->last_B = -1;  // the device work list is gone
     m->ws = nullptr;
   }
   if (hipMalloc(&m->ws, off) != hipSuccess) {
@@ -310,8 +308,7 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   m->out = (float*)(base + o_out);
   m->norm = (float*)(base + o_norm);
   m->ids = (uint32_t*)(base + o_ids);
-  m->cu = (int*)(base + o_cu);
-  m->work = (int2*)(base + o_work);
+  m->work = (int4*)(base + o_work);
   m->rec0 = (float*)(base + o_rec);
   m->rec1 = m->rec0 + (size_t)tpad * NORM_REC_GEMV;
   m->cap_tokens = tpad - 128;
@@ -457,19 +454,19 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   return T5H_OK;
 }
 
-// Uploads cu_seqlens and the attention work list through a pinned staging slot.
+// Uploads the attention work list through a pinned staging slot: one (start, length, query
+// tile) item per 64 queries of a sequence, so the kernel needs no further lookup.
 int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   nwork = 0;
   for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
   // The same batch layout as the previous upload (e.g. a stream of equal-length queries):
-  // the device copies of cu_seqlens and the work list are still current.
+  // the device copy of the work list is still current.
   if (B == m->last_B && std::equal(cu, cu + B + 1, m->last_cu.begin())) return T5H_OK;
   m->last_B = -1;
   StagingSlot& s = m->slots[m->next_slot];
   m->next_slot = (m->next_slot + 1) % 4;
   if (s.used) HIP_OK(hipEventSynchronize(s.done));
-  const size_t wofs = ((size_t)(B + 1) * 4 + 7) & ~(size_t)7;  // work list is 8-byte aligned
-  const size_t need = wofs + (size_t)nwork * 8;
+  const size_t need = (size_t)nwork * sizeof(int4);
   if (need > s.cap) {
     if (s.host) (void)hipHostFree(s.host);
     s.host = nullptr;
@@ -479,9 +476,7 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
     s.cap = std::max(need, (size_t)4096);
   }
   if (!s.done) HIP_OK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
-  int* hc = (int*)s.host;
-  memcpy(hc, cu, (size_t)(B + 1) * 4);
-  int2* hw = (int2*)((uint8_t*)s.host + wofs);
+  int4* hw = (int4*)s.host;
   // Longest sequences first (every query tile of a sequence costs ceil(L/64) key tiles), so
   // the attention grid drains with its cheapest workgroups.
   m->order.resize(B);
@@ -493,10 +488,9 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   for (int b : m->order) {
     m->attn_flops += 4.0 * (double)(cu[b + 1] - cu[b]) * (cu[b + 1] - cu[b]) * m->cfg.d_kv * m->cfg.num_heads;
     const int L = cu[b + 1] - cu[b];
-    for (int q = 0; q * 64 < L; q++) hw[w++] = make_int2(b, q);
+    for (int q = 0; q * 64 < L; q++) hw[w++] = make_int4(cu[b], L, q * 64, 0);
   }
-  HIP_OK(hipMemcpyAsync(m->cu, hc, (size_t)(B + 1) * 4, hipMemcpyHostToDevice, m->stream));
-  if (nwork) HIP_OK(hipMemcpyAsync(m->work, hw, (size_t)nwork * 8, hipMemcpyHostToDevice, m->stream));
+  if (nwork) HIP_OK(hipMemcpyAsync(m->work, hw, (size_t)nwork * sizeof(int4), hipMemcpyHostToDevice, m->stream));
   HIP_OK(hipEventRecord(s.done, m->stream));
   s.used = true;
   m->last_cu.assign(cu, cu + B + 1);
@@ -584,7 +578,6 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     AttnArgs a{};
     a.qkv = m->qkvb;
     a.out = m->ao;
-    a.cu = m->cu;
     a.work = m->work;
     a.lut = m->rel_lut;
     a.heads = c.num_heads;
