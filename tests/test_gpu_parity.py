@@ -491,6 +491,46 @@ def test_folded_norm_survives_residual_growth(enc_mod):
             x_last = ora.hidden(ids[s:e], 3)  # input of the last block: the grown residual
             assert np.sqrt((x_last.astype(np.float64) ** 2).mean()) > 1e3
             assert cos_rows(a[s:e], ora.forward(ids[s:e])).min() >= COS_MIN, k
+        # the query path (GEMV kernels, 64-float records) under the same growth
+        for L in (5, 32, 64):
+            q = np.random.default_rng(40 + L).integers(1, cfg["vocab_size"], size=L).astype(np.uint32)
+            qc = np.array([0, L], np.int32)
+            a, _ = gpu.encode_packed(q, qc)
+            b, _ = unfolded.encode_packed(q, qc)
+            assert np.isfinite(a).all(), L
+            assert cos_rows(a, b).min() >= 0.9999, L
+            assert cos_rows(a, ora.forward(q)).min() >= COS_MIN, L
     finally:
         unfolded.close()
         gpu.close()
+
+
+@pytest.mark.parametrize("layout", ["q4k", "hybrid"])
+def test_folded_norm_query_path(enc_mod, layout):
+    """Small token counts run the GEMV kernels, which fold each T5LayerNorm with one partial sum
+    per 16 columns (the small model's d_model 256: 16 partials, XTR-base: 48).  Against the
+    GEMV kernels with the norm computed in the consumer (T5H_FOLD_NORM=0): same results at f16
+    operand precision; both within the oracle bar; deterministic across calls."""
+    for cfg, seed in ((synth.small_config(), 61), (dict(synth.XTR_BASE, num_layers=3), 62)):
+        img = synth.make_model(cfg, seed=seed, layout=layout)
+        gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+        unfolded = _handle_with_env(enc_mod, img, cfg, T5H_FOLD_NORM="0")
+        ora = orc.OracleModel(img, cfg)
+        try:
+            for lens in ([1], [32], [17, 40], [64]):
+                cu = np.zeros(len(lens) + 1, np.int32)
+                cu[1:] = np.cumsum(lens)
+                ids = np.random.default_rng(seed + int(cu[-1])).integers(
+                    1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+                a, _ = gpu.encode_packed(ids, cu)
+                b, _ = unfolded.encode_packed(ids, cu)
+                assert rel(a, b) <= CROSS_PATH_REL, (cfg["d_model"], lens, rel(a, b))
+                assert cos_rows(a, b).min() >= 0.9999, (cfg["d_model"], lens)
+                a2, _ = gpu.encode_packed(ids, cu)
+                assert np.array_equal(a, a2)
+                for k in range(len(lens)):
+                    s, e = int(cu[k]), int(cu[k + 1])
+                    assert cos_rows(a[s:e], ora.forward(ids[s:e])).min() >= COS_MIN, (cfg["d_model"], lens, k)
+        finally:
+            unfolded.close()
+            gpu.close()
