@@ -46,25 +46,27 @@ __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* V
                                           const h8 (&qf)[2], int k0, int L, float& m_run, float& l_run,
                                           f4 (&o)[4]) {
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-  // S^T[key][query] for the valid key blocks of 16
+  // S^T[key][query] + bias for the valid key blocks of 16: the accumulators start from the
+  // bias, so the matrix core does the add
   f4 s[4];
 #pragma unroll
   for (int kb = 0; kb < 4; kb++) {
     s[kb] = f4{0.f, 0.f, 0.f, 0.f};
     if (kb >= NKB) continue;
 #pragma unroll
+    for (int i = 0; i < 4; i++) s[kb][i] = Bsb[bofs + kb * 16 + i];
+#pragma unroll
     for (int ds = 0; ds < 2; ds++) {
       const h8 a = *reinterpret_cast<const h8*>(&Ksb[(kb * 16 + lr) * KPAD + ds * 32 + lg * 8]);
       s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
     }
   }
-  // bias, mask, running max
+  // mask, running max
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      s[kb][i] += Bsb[bofs + kb * 16 + i];
       if (MASK && k0 + kb * 16 + lg * 4 + i >= L) s[kb][i] = -INFINITY;
       mx = fmaxf(mx, s[kb][i]);
     }
