@@ -534,3 +534,21 @@ def test_folded_norm_query_path(enc_mod, layout):
         finally:
             unfolded.close()
             gpu.close()
+
+
+def test_wide_model_runs_standalone_norms(enc_mod):
+    """d_model 1024 does not fit a norm record (at most 15 x 64 columns), so both paths fall back
+    to the unfolded norms: the batched path launches the standalone RMSNorm, the GEMV path
+    normalises inside the consuming kernel.  Both against the oracle."""
+    cfg = synth.small_config(d_model=1024, d_ff=1024, num_heads=16, num_layers=2)
+    img = synth.make_model(cfg, seed=71)
+    gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    ora = orc.OracleModel(img, cfg)
+    try:
+        for lens in ([80, 130], [20], [64]):
+            cu = np.zeros(len(lens) + 1, np.int32)
+            cu[1:] = np.cumsum(lens)
+            ids = np.random.default_rng(int(cu[-1])).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+            _check_batch(gpu, ora, ids, cu)
+    finally:
+        gpu.close()
