@@ -246,12 +246,15 @@ def score_bench(args) -> None:
     qs = _event_time(torch, qstep, args.steps)
     q_bytes = N * D // 2 + M * D * 4 + M * N * 4
     q_tf = 2.0 * M * N * D / qs / 1e12
-    q4 = {"kernel": "matmul_t_q4_stream_kernel (codes -> LDS table -> v_mfma_f32_16x16x4_f32)",
-          "avg_launch_us": qs * 1e6, "bytes_per_launch": q_bytes, "gbs": q_bytes / qs / 1e9,
-          "hbm_frac": q_bytes / qs / 1e9 / PEAK_HBM_GBS, "tflops": q_tf, "mfma_frac": q_tf / PEAK_F32_MFMA_TFLOPS,
+    # bf16 MFMAs with both operands split in three parts: 6 bf16 products per f32 product
+    q4 = {"kernel": "matmul_t_q4_split_kernel (code bytes -> LDS table of bf16 hi/mid/lo pairs -> "
+                    "6 x v_mfma_f32_16x16x32_bf16 per block)",
+          "bound": "hbm", "avg_launch_us": qs * 1e6, "bytes_per_launch": q_bytes, "gbs": q_bytes / qs / 1e9,
+          "hbm_frac": q_bytes / qs / 1e9 / PEAK_HBM_GBS, "tflops_f32_equivalent": q_tf,
+          "bf16_mfma_frac": 6 * q_tf / PEAK_F16_TFLOPS,
           "scores_per_s": M * N / qs, "speedup_vs_f32_residuals": avg_s / qs}
     log(f"[bench] score from q4 codes: {qs * 1e6:.1f} us/launch ({avg_s / qs:.2f}x the f32 residuals), "
-        f"{q_bytes / qs / 1e9:.0f} GB/s, {q_tf:.1f} TFLOP/s f32")
+        f"{q_bytes / qs / 1e9:.0f} GB/s, {q_tf:.1f} TFLOP/s f32-equivalent")
 
     # Index build: residual codes of N embeddings against their assigned centres
     # (src/lib.rs:1375-1376): N*512 B in, N*64 B out (centres stay in L2).

@@ -135,3 +135,28 @@ def test_matmul_t_q4_matches_decode_then_matmul(codec):
 def test_matmul_t_q4_shape_errors(codec):
     with pytest.raises(ValueError):
         codec.matmul_t_q4(np.zeros((2, 128), np.float32), np.zeros((3, 32), np.uint8))
+
+
+def test_matmul_t_q4_nonfinite_query(codec):
+    """The streaming shape runs on bf16 MFMAs with both operands split in three parts, which
+    cannot carry infinities (inf times parts of both signs would give NaN); a query block with a
+    non-finite value takes the f32 kernel.  The NaN / inf pattern then equals the two-step f32
+    result, and the finite rows of the same launch stay within the summation bound."""
+    from witchcraft_amd import score
+    rng = np.random.default_rng(31)
+    a = _unit_rows(20, 128, rng)
+    a[3, 7] = np.inf
+    a[5, 100] = -np.inf
+    a[9, 0] = np.nan
+    codes = rng.integers(0, 256, (4096, 64)).astype(np.uint8)
+    got = codec.matmul_t_q4(a, codes)
+    two_step = score.matmul_t(a, codec.from_companded_q4_bytes(codes, 128))
+    assert np.array_equal(np.isnan(got), np.isnan(two_step))
+    inf = np.isinf(two_step)
+    assert np.array_equal(np.isinf(got), inf)
+    assert np.array_equal(np.sign(got[inf]), np.sign(two_step[inf]))
+    fin = [i for i in range(20) if i not in (3, 5, 9)]
+    r = orc.residual_decode(codes, 128).astype(np.float64)
+    want = a[fin].astype(np.float64) @ r.T
+    bound = 128 * 2.0 ** -23 * (np.abs(a[fin]).astype(np.float64) @ np.abs(r).T)
+    assert np.all(np.abs(got[fin] - want) <= bound)

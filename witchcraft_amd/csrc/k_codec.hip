@@ -19,6 +19,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace t5k {
 struct Q4Table {
@@ -104,12 +105,18 @@ __global__ __launch_bounds__(256) void residual_decode_kernel(const uint8_t* __r
 // k = 32 lg + 4 s + j in step s; A is read from LDS with the same assignment, so every product
 // appears once.  C[m][n] for rows n >= N is computed from zero bytes and never stored.
 template <int MB>
-__global__ __launch_bounds__(256, 2) void matmul_t_q4_stream_kernel(const float* __restrict__ A,
-                                                                    const uint8_t* __restrict__ codes, Q4Table tab,
-                                                                    float* __restrict__ C, int M, int N) {
+struct Q4StreamLds {
+  float4 As[16 * MB * (128 / 4 + 1)];
+  float lut[16];
+};
+
+template <int MB>
+__device__ __forceinline__ void q4_stream_f32(const float* __restrict__ A, const uint8_t* __restrict__ codes,
+                                              const Q4Table& tab, float* __restrict__ C, int M, int N,
+                                              Q4StreamLds<MB>& sh) {
   constexpr int D = 128, AS = D / 4 + 1;
-  __shared__ float4 As[16 * MB * AS];
-  __shared__ float lut[16];
+  float4* As = sh.As;
+  float* lut = sh.lut;
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   const int w0 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = gridDim.x * 4;
   const int ntiles = (N + 31) / 32, nfull = N / 32, tail_bytes = (N % 32) * (D / 2);
@@ -169,6 +176,183 @@ __global__ __launch_bounds__(256, 2) void matmul_t_q4_stream_kernel(const float*
   };
   // Same issue order as matmul_t_stream_kernel: next tile's loads, previous tile's stores,
   // this tile's MFMAs, two tiles per trip.
+  uint4 b0[2], b1[2];
+  f4v acc0[MB][2], acc1[MB][2];
+  int t = w0, t1 = -1;
+  load(t, b0);
+  while (t < ntiles) {
+    load(t + nw, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t1 >= 0) store(t1, acc1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b0, acc0);
+    const int t0 = t;
+    t += nw;
+    t1 = -1;
+    if (t >= ntiles) {
+      store(t0, acc0);
+      break;
+    }
+    load(t + nw, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    store(t0, acc0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b1, acc1);
+    t1 = t;
+    t += nw;
+  }
+  if (t1 >= 0) store(t1, acc1);
+}
+
+template <int MB>
+__global__ __launch_bounds__(256, 2) void matmul_t_q4_stream_kernel(const float* __restrict__ A,
+                                                                    const uint8_t* __restrict__ codes, Q4Table tab,
+                                                                    float* __restrict__ C, int M, int N) {
+  __shared__ Q4StreamLds<MB> sh;
+  q4_stream_f32<MB>(A, codes, tab, C, M, N, sh);
+}
+
+// The same stream on bf16 MFMAs.  v_mfma_f32_16x16x32_bf16 runs 8x the FLOPs of
+// v_mfma_f32_16x16x4_f32 in half the cycles, so each f32 operand is split into three bf16
+// parts, x = x_hi + x_mid + x_lo (round to nearest each; the parts hold 24 significant bits,
+// |x - sum| <= 2^-27 |x|), and a product is taken as the six part products with i + j <= 2 --
+// the three dropped ones are below 2^-25 |a t|.  Each part product is exact in f32, so the
+// result stays within the f32 summation bound of the f32 kernel, at 6 x 16 = 96 cycles of
+// matrix core per 16 x 16 x 32 block instead of 8 x 32 = 256.
+//  * Residual side (A operand): a 256-entry LDS table maps a code byte to the split parts of
+//    its two values, (t[hi nibble], t[lo nibble]) packed as bf16 pairs -- hi pair, mid pair,
+//    lo pair -- so a lane's 8 values of a 32-wide K slice (4 code bytes) are 4 table reads and
+//    no packing.  Lane (lr, lg) keeps the f32 kernel's rows lr and 16 + lr and bytes
+//    16 lg .. 16 lg + 15 (k = 32 lg .. 32 lg + 31); K slice s uses bytes 16 lg + 4 s .. + 3,
+//    i.e. k = 32 lg + 8 s + 0 .. 7 in MFMA slots 8 lg .. 8 lg + 7.
+//  * Query side (B operand): the same k for query row lr, split once at kernel start and held
+//    in registers (48 per 16 query rows).
+//  * A query block with a non-finite value takes the f32 kernel instead: inf times a split
+//    table value can meet parts of both signs and turn into NaN where f32 gives inf.
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;  // finite x
+}
+// x = hi + mid + lo as bf16 bit patterns
+__device__ __forceinline__ void split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = bf16_rne_bits(x);
+  const float r1 = x - __uint_as_float(hi << 16);
+  mid = bf16_rne_bits(r1);
+  const float r2 = r1 - __uint_as_float(mid << 16);
+  lo = bf16_rne_bits(r2);
+}
+
+template <int MB>
+__global__ __launch_bounds__(256, 2) void matmul_t_q4_split_kernel(const float* __restrict__ A,
+                                                                   const uint8_t* __restrict__ codes, Q4Table tab,
+                                                                   float* __restrict__ C, int M, int N) {
+  constexpr int D = 128;
+  __shared__ uint4 pt[256];
+  __shared__ Q4StreamLds<MB> sh;
+  __shared__ int bad;
+  if (threadIdx.x == 0) bad = 0;
+  __syncthreads();
+  {
+    // byte x -> parts of (t[x >> 4], t[x & 15]); the first value takes the low half (lower k)
+    const int x = threadIdx.x;
+    uint32_t h0, m0, l0, h1, m1, l1;
+    split3(tab.v[x >> 4], h0, m0, l0);
+    split3(tab.v[x & 15], h1, m1, l1);
+    pt[x] = make_uint4(h0 | (h1 << 16), m0 | (m1 << 16), l0 | (l1 << 16), 0u);
+    int nf = 0;
+    for (int e = threadIdx.x; e < 16 * MB * D; e += 256) {
+      const int r = e / D;
+      if (r < M && !__builtin_isfinite(A[(size_t)r * D + (e - r * D)])) nf = 1;
+    }
+    if (nf) bad = 1;  // every writer stores 1
+  }
+  __syncthreads();
+  if (bad) {
+    q4_stream_f32<MB>(A, codes, tab, C, M, N, sh);
+    return;
+  }
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int w0 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = gridDim.x * 4;
+  const int ntiles = (N + 31) / 32, nfull = N / 32, tail_bytes = (N % 32) * (D / 2);
+
+  // query parts: q[i][s][p] = part p of query row 16 i + lr, k = 32 lg + 8 s .. + 7
+  uint4 q[MB][4][3];
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const float* row = A + (size_t)min(16 * i + lr, M - 1) * D + 32 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const float4 u = *reinterpret_cast<const float4*>(row + 8 * s);
+      const float4 v = *reinterpret_cast<const float4*>(row + 8 * s + 4);
+      const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+      uint32_t hp[8], mp[8], lp[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) split3(x[j], hp[j], mp[j], lp[j]);
+      q[i][s][0] = make_uint4(hp[0] | (hp[1] << 16), hp[2] | (hp[3] << 16), hp[4] | (hp[5] << 16), hp[6] | (hp[7] << 16));
+      q[i][s][1] = make_uint4(mp[0] | (mp[1] << 16), mp[2] | (mp[3] << 16), mp[4] | (mp[5] << 16), mp[6] | (mp[7] << 16));
+      q[i][s][2] = make_uint4(lp[0] | (lp[1] << 16), lp[2] | (lp[3] << 16), lp[4] | (lp[5] << 16), lp[6] | (lp[7] << 16));
+    }
+  }
+
+  const int voff[2] = {lr * (D / 2) + 16 * lg, (16 + lr) * (D / 2) + 16 * lg};
+  auto load = [&](int t, uint4 (&b)[2]) {
+    const int bytes = t < nfull ? 32 * (D / 2) : (t == nfull ? tail_bytes : 0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(codes + (size_t)t * 32 * (D / 2)), (short)0, bytes, kBufDword3);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const f4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[nb], 0, 0);
+      b[nb] = __builtin_bit_cast(uint4, v);
+    }
+  };
+  auto mm = [](const uint4& a, const uint4& b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8v, a), __builtin_bit_cast(bf8v, b), c, 0, 0, 0);
+  };
+  auto compute = [&](const uint4 (&b)[2], f4v (&acc)[MB][2]) {
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) acc[i][nb] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const uint32_t w = s == 0 ? b[nb].x : s == 1 ? b[nb].y : s == 2 ? b[nb].z : b[nb].w;
+        const uint4 e0 = pt[w & 255], e1 = pt[(w >> 8) & 255], e2 = pt[(w >> 16) & 255], e3 = pt[w >> 24];
+        const uint4 rh = make_uint4(e0.x, e1.x, e2.x, e3.x);
+        const uint4 rm = make_uint4(e0.y, e1.y, e2.y, e3.y);
+        const uint4 rl = make_uint4(e0.z, e1.z, e2.z, e3.z);
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+          f4v c = acc[i][nb];
+          c = mm(rh, q[i][s][0], c);
+          c = mm(rh, q[i][s][1], c);
+          c = mm(rm, q[i][s][0], c);
+          c = mm(rh, q[i][s][2], c);
+          c = mm(rm, q[i][s][1], c);
+          c = mm(rl, q[i][s][0], c);
+          acc[i][nb] = c;
+        }
+      }
+  };
+  int soff[MB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) soff[i] = ((16 * i + lr) * N + 4 * lg) * 4;
+  auto store = [&](int t, const f4v (&acc)[MB][2]) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(C + (size_t)t * 32), (short)0, 0x7fffffff, kBufDword3);
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+      const bool row_ok = 16 * i + lr < M;
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+        if (row_ok && 32 * t + 16 * nb + 4 * lg < N)
+          __builtin_amdgcn_raw_buffer_store_b128(acc[i][nb], rs, soff[i] + 64 * nb, 0, 0);
+    }
+  };
+  // the f32 kernel's issue order: next tile's loads, previous tile's stores, this tile's MFMAs
   uint4 b0[2], b1[2];
   f4v acc0[MB][2], acc1[MB][2];
   int t = w0, t1 = -1;
@@ -294,8 +478,18 @@ hipError_t launch_matmul_t_q4(const float* A, const uint8_t* codes, const Q4Tabl
   const bool aligned = ((uintptr_t)A & 15) == 0 && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)C & 15) == 0;
   if (D == 128 && M <= 32 && N % 4 == 0 && N >= 4096 && aligned && (size_t)N * 4 * 32 < 0x7fffffffu) {
     const int wgs = std::min(2 * num_cus_codec(), (N + 127) / 128);
-    if (M <= 16) hipLaunchKernelGGL((matmul_t_q4_stream_kernel<1>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
-    else hipLaunchKernelGGL((matmul_t_q4_stream_kernel<2>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+    // T5H_Q4_SCORE_F32=1 keeps the f32-MFMA stream (measurement and tests)
+    static const bool f32_only = [] {
+      const char* e = getenv("T5H_Q4_SCORE_F32");
+      return e && atoi(e) == 1;
+    }();
+    if (f32_only) {
+      if (M <= 16) hipLaunchKernelGGL((matmul_t_q4_stream_kernel<1>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+      else hipLaunchKernelGGL((matmul_t_q4_stream_kernel<2>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+    } else {
+      if (M <= 16) hipLaunchKernelGGL((matmul_t_q4_split_kernel<1>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+      else hipLaunchKernelGGL((matmul_t_q4_split_kernel<2>), dim3(wgs), dim3(256), 0, s, A, codes, tab, C, M, N);
+    }
     return hipGetLastError();
   }
   const dim3 grid((N + 63) / 64, (M + 63) / 64);
