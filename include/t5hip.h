@@ -150,7 +150,9 @@ int t5h_residual_encode_device(const float* d_emb, int32_t N, const float* d_cen
 int t5h_residual_decode(int32_t hip_device, const uint8_t* codes, int32_t N, int32_t D, float* out);
 int t5h_residual_decode_device(const uint8_t* d_codes, int32_t N, int32_t D, float* d_out, void* stream);
 /* Search-time residual scores without materialising the residuals (src/lib.rs:676-680,734-735):
- * C[M][N] = A[M][D] . from_companded_q4_bytes(codes)[N][D]^T in f32, D % 4 == 0. */
+ * C[M][N] = A[M][D] . from_companded_q4_bytes(codes)[N][D]^T, D % 4 == 0, within the f32
+ * summation bound D * 2^-23 * sum |a||r| of the f32 product (query-sized A against many rows
+ * runs on bf16 MFMAs with both operands split in three parts; non-finite queries on f32). */
 int t5h_matmul_t_q4(int32_t hip_device, const float* a, int32_t M, const uint8_t* codes, int32_t N, int32_t D,
                     float* c);
 int t5h_matmul_t_q4_device(const float* d_a, int32_t M, const uint8_t* d_codes, int32_t N, int32_t D, float* d_c,
