@@ -552,3 +552,20 @@ def test_wide_model_runs_standalone_norms(enc_mod):
             _check_batch(gpu, ora, ids, cu)
     finally:
         gpu.close()
+
+
+def test_tile_width_does_not_change_bits(enc_mod, xtr):
+    """Every batched GEMM accumulates K in the same order whatever its tile width, and the folded
+    norm's partial sums are kept per 64 columns whatever the tile width: BN = 64 and BN = 128
+    (T5H_GEMM_BN) give the same bits as the measured plan."""
+    cfg, img, gpu, _ = xtr
+    hs = {bn: _handle_with_env(enc_mod, img, cfg, T5H_GEMM_BN=bn) for bn in ("64", "128")}
+    try:
+        ids, cu = synth.ragged_batch(20, 32, 256, cfg["vocab_size"], seed=88)
+        ref, _ = gpu.encode_packed(ids, cu)
+        for bn, h in hs.items():
+            got, _ = h.encode_packed(ids, cu)
+            assert np.array_equal(got, ref), bn
+    finally:
+        for h in hs.values():
+            h.close()
