@@ -34,14 +34,20 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
   if (fmt == EMB_F32 || bad) {
     // lane holds columns 4i .. 4i+3, i = lane + 64j
     const float4* src = reinterpret_cast<const float4*>((const float*)table + (size_t)(bad ? 0 : id) * D);
-    float4 v[EMB_NORM_MAX_D / 256];
+    float4 v[EMB_NORM_MAX_D / 256], g[EMB_NORM_MAX_D / 256];
     float ss = 0.f;
     if (rec) {
+      // the row and gamma are requested together: one memory round trip before the sum
 #pragma unroll
       for (int j = 0; j < EMB_NORM_MAX_D / 256; j++) {
         const int i = lane + 64 * j;
-        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        v[j] = g[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (i < D / 4 && !bad) v[j] = src[i];
+        if (i < D / 4) g[j] = reinterpret_cast<const float4*>(gamma)[i];
+      }
+#pragma unroll
+      for (int j = 0; j < EMB_NORM_MAX_D / 256; j++) {
+        const int i = lane + 64 * j;
         if (i < D / 4) reinterpret_cast<float4*>(xr)[i] = v[j];
         ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
       }
@@ -52,10 +58,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
       for (int j = 0; j < EMB_NORM_MAX_D / 256; j++) {
         const int i = lane + 64 * j;
         if (i >= D / 4) continue;
-        const float4 g = reinterpret_cast<const float4*>(gamma)[i];
         *reinterpret_cast<h4*>(xn + tiled_index(t, 4 * i, D)) =
-            h4{(_Float16)((v[j].x * g.x) * sc), (_Float16)((v[j].y * g.y) * sc), (_Float16)((v[j].z * g.z) * sc),
-               (_Float16)((v[j].w * g.w) * sc)};
+            h4{(_Float16)((v[j].x * g[j].x) * sc), (_Float16)((v[j].y * g[j].y) * sc),
+               (_Float16)((v[j].z * g[j].z) * sc), (_Float16)((v[j].w * g[j].w) * sc)};
       }
       if (lane < rs / 4) {
         float4* d = reinterpret_cast<float4*>(rec + (size_t)t * rs) + lane;
@@ -93,9 +98,14 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
     for (int e = lane; e < D; e += 64) xr[e] = deq(e);
     return;
   }
-  // lane holds columns lane + 64j
-  float v[EMB_NORM_MAX_D / 64];
+  // lane holds columns lane + 64j; gamma is requested with the table bytes
+  float v[EMB_NORM_MAX_D / 64], g[EMB_NORM_MAX_D / 64];
   float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < EMB_NORM_MAX_D / 64; j++) {
+    const int e = lane + 64 * j;
+    g[j] = e < D ? gamma[e] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < EMB_NORM_MAX_D / 64; j++) {
     const int e = lane + 64 * j;
@@ -111,7 +121,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 #pragma unroll
   for (int j = 0; j < EMB_NORM_MAX_D / 64; j++) {
     const int e = lane + 64 * j;
-    if (e < D) xn[tiled_index(t, e, D)] = (_Float16)((v[j] * gamma[e]) * sc);
+    if (e < D) xn[tiled_index(t, e, D)] = (_Float16)((v[j] * g[j]) * sc);
   }
   if (lane < rs / 4) {
     float4* d = reinterpret_cast<float4*>(rec + (size_t)t * rs) + lane;
