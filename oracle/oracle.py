@@ -6,7 +6,6 @@ cpu_baseline leg, as the checker -- never by the witchcraft_amd product path.
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 
 import numpy as np
@@ -48,6 +47,8 @@ def _load() -> C.CDLL:
     u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
     u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
     i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+    lib.orc_set_threads.argtypes = [C.c_int]
+    lib.orc_max_threads.restype = C.c_int
     lib.orc_f16_to_f32.argtypes = [C.c_uint16]
     lib.orc_f16_to_f32.restype = C.c_float
     lib.orc_q4k_dequant.argtypes = [u8p, C.c_size_t, f32p]
@@ -107,9 +108,11 @@ def lib() -> C.CDLL:
     return _lib
 
 
-def set_threads(n: int) -> None:
-    """OpenMP thread count of the oracle (must be called before its first parallel region)."""
-    os.environ["OMP_NUM_THREADS"] = str(n)
+def set_threads(n: int) -> int:
+    """Sets the OpenMP thread count of the oracle's parallel loops; returns the count they
+    will use, as the OpenMP runtime reports it."""
+    lib().orc_set_threads(int(n))
+    return int(lib().orc_max_threads())
 
 
 # ---- block codecs / scalar ops ------------------------------------------------------

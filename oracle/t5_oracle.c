@@ -26,6 +26,11 @@
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
+
+void orc_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+}
+int orc_max_threads(void) { return omp_get_max_threads(); }
 #endif
 
 #define QK_K 256

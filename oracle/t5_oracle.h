@@ -41,6 +41,9 @@ typedef struct {
 typedef struct orc_model orc_model;
 
 /* ---- block codecs ---- */
+/* OpenMP threads of the oracle's parallel loops: set, and read back what they will use. */
+void orc_set_threads(int n);
+int orc_max_threads(void);
 float orc_f16_to_f32(uint16_t h);
 void orc_get_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m);
 void orc_q4k_dequant(const uint8_t* blocks, size_t nblk, float* out);

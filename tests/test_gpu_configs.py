@@ -1,0 +1,165 @@
+"""The benchmark's own batches through the HIP path, at their full workload size.
+
+cfg2 (32 sequences, L ~ U[32, 256]), cfg4 (256 sequences, L ~ U[64, 512], ~71k tokens) and
+cfg5 (hybrid layout, 64 sequences, L ~ U[16, 512]) are drawn exactly as bench.py draws them
+(model seed 0, batch seed 1000).  The reference encodes each sequence alone as [1, L]
+(src/embedder.rs:40-41), so the packed batch must reproduce per-sequence results:
+  * every output finite and the whole batch deterministic across calls;
+  * sequences encoded alone bit-identical to their rows inside the batch (sequences longer
+    than the small-token cutoff, so both runs take the batched GEMM path);
+  * per-token cosine >= 0.999 against the oracle on every cfg2 sequence and on 16 sequences
+    of cfg4 / cfg5 including the longest.
+Plus the per-layer bar (relative error <= 1e-3, teacher-forced) on all 12 XTR-base blocks on
+both the batched and the small-token path (src/quantized_t5.rs:598-627).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from witchcraft_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999
+LAYER_REL = 1e-3
+GEMV_MAX_M = 64
+BATCH_SEED = 1000  # bench.py: ragged_batch(..., seed=1000 + --seed)
+
+
+def cos_rows(a, b):
+    return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+
+
+def rel(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b.astype(np.float64)))
+
+
+def _model(layout):
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg = dict(synth.XTR_BASE)
+    img = synth.make_model(cfg, seed=0, layout=layout)
+    return cfg, img, T5EncoderModel.from_gguf(img, cfg)
+
+
+@pytest.fixture(scope="module")
+def xtr():
+    cfg, img, gpu = _model("q4k")
+    yield cfg, img, gpu, orc.OracleModel(img, cfg)
+    gpu.close()
+
+
+@pytest.fixture(scope="module")
+def xtr_hybrid():
+    cfg, img, gpu = _model("hybrid")
+    yield cfg, img, gpu, orc.OracleModel(img, cfg)
+    gpu.close()
+
+
+def _sample(cu, n, seed):
+    """n sequence indices: the longest, the shortest, and n - 2 drawn at random."""
+    lens = np.diff(cu)
+    pick = {int(np.argmax(lens)), int(np.argmin(lens))}
+    rng = np.random.default_rng(seed)
+    for b in rng.permutation(lens.size):
+        if len(pick) >= n:
+            break
+        pick.add(int(b))
+    return sorted(pick)
+
+
+def _vs_oracle(ora, ids, cu, out, seqs, tag):
+    worst = 1.0
+    for b in seqs:
+        s, e = int(cu[b]), int(cu[b + 1])
+        c = cos_rows(out[s:e], ora.forward(ids[s:e]))
+        worst = min(worst, float(c.min()))
+        assert c.min() >= COS_MIN, (tag, b, e - s, float(c.min()))
+    print(f"[{tag}] {len(seqs)} sequences vs oracle, min cosine {worst:.6f}", flush=True)
+
+
+def _properties(gpu, ids, cu, out, tag, n_alone=10):
+    assert np.isfinite(out).all(), tag
+    out2, _ = gpu.encode_packed(ids, cu)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32)), f"{tag}: not deterministic"
+    lens = np.diff(cu)
+    cand = [b for b in _sample(cu, 3 * n_alone, 7) if lens[b] > GEMV_MAX_M][:n_alone]
+    for b in cand:
+        s, e = int(cu[b]), int(cu[b + 1])
+        alone, _ = gpu.encode_packed(ids[s:e], np.array([0, e - s], np.int32))
+        assert np.array_equal(alone.view(np.uint32), out[s:e].view(np.uint32)), (tag, b, e - s)
+    print(f"[{tag}] T={int(cu[-1])}: finite, deterministic, {len(cand)} sequences alone bit-identical",
+          flush=True)
+
+
+@pytest.fixture(scope="module")
+def cfg4_run(xtr):
+    cfg, _, gpu, _ = xtr
+    ids, cu = synth.ragged_batch(256, 64, 512, cfg["vocab_size"], seed=BATCH_SEED)
+    out, norms = gpu.encode_packed(ids, cu)
+    return ids, cu, out, norms
+
+
+@pytest.fixture(scope="module")
+def cfg5_run(xtr_hybrid):
+    cfg, _, gpu, _ = xtr_hybrid
+    ids, cu = synth.ragged_batch(64, 16, 512, cfg["vocab_size"], seed=BATCH_SEED)
+    out, norms = gpu.encode_packed(ids, cu)
+    return ids, cu, out, norms
+
+
+def test_cfg2_bench_batch_every_sequence_vs_oracle(xtr):
+    cfg, _, gpu, ora = xtr
+    ids, cu = synth.ragged_batch(32, 32, 256, cfg["vocab_size"], seed=BATCH_SEED)
+    out, norms = gpu.encode_packed(ids, cu)
+    assert np.isfinite(out).all()
+    assert np.allclose(norms, np.linalg.norm(out, axis=1), rtol=1e-5)
+    _vs_oracle(ora, ids, cu, out, range(32), "cfg2")
+
+
+def test_cfg4_bench_batch_properties(xtr, cfg4_run):
+    _, _, gpu, _ = xtr
+    ids, cu, out, norms = cfg4_run
+    assert cu.size == 257 and cu[-1] > 60000
+    assert np.allclose(norms, np.linalg.norm(out, axis=1), rtol=1e-5)
+    _properties(gpu, ids, cu, out, "cfg4")
+
+
+def test_cfg4_bench_batch_vs_oracle(xtr, cfg4_run):
+    _, _, _, ora = xtr
+    ids, cu, out, _ = cfg4_run
+    _vs_oracle(ora, ids, cu, out, _sample(cu, 16, 11), "cfg4")
+
+
+def test_cfg5_bench_batch_properties(xtr_hybrid, cfg5_run):
+    _, _, gpu, _ = xtr_hybrid
+    ids, cu, out, _ = cfg5_run
+    assert cu.size == 65 and np.diff(cu).max() > 256
+    _properties(gpu, ids, cu, out, "cfg5")
+
+
+def test_cfg5_bench_batch_vs_oracle(xtr_hybrid, cfg5_run):
+    _, _, _, ora = xtr_hybrid
+    ids, cu, out, _ = cfg5_run
+    _vs_oracle(ora, ids, cu, out, _sample(cu, 16, 12), "cfg5")
+
+
+@pytest.mark.parametrize("lens", [[96, 130], [32]], ids=["batched", "gemv"])
+def test_all_layers_teacher_forced(xtr, lens):
+    """Every block gets the oracle's input (the oracle's output of the block before) and must
+    reproduce the oracle's output within 1e-3 relative, per token and overall."""
+    cfg, _, gpu, ora = xtr
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = np.random.default_rng(sum(lens)).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    xs = [ora.hidden(ids[cu[b]:cu[b + 1]], 0) for b in range(len(lens))]
+    worst = 0.0
+    for layer in range(cfg["num_layers"]):
+        x_in = np.concatenate(xs)
+        y = gpu.layer_forward(layer, x_in, cu)
+        xs = [ora.layer(layer, x) for x in xs]
+        y_ref = np.concatenate(xs)
+        per_tok = np.linalg.norm(y - y_ref, axis=1) / np.linalg.norm(y_ref, axis=1)
+        worst = max(worst, float(per_tok.max()))
+        assert rel(y, y_ref) <= LAYER_REL, (layer, rel(y, y_ref))
+        assert per_tok.max() <= LAYER_REL, (layer, float(per_tok.max()))
+    print(f"[layers {lens}] worst per-token relative error over 12 blocks {worst:.2e}", flush=True)

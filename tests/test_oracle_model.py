@@ -169,3 +169,19 @@ def test_missing_tensor_is_an_error():
     del ts["encoder.final_layer_norm.weight"]
     with pytest.raises(ValueError, match="missing tensor"):
         orc.OracleModel(gguf.write_gguf(list(ts.values())), cfg)
+
+
+def test_torch_cpu_port_matches_oracle():
+    """The torch-CPU f32 restatement that bench.py times as the strong-BLAS CPU baseline computes
+    the same encoder as the C oracle (float64 accumulation): f32 rounding only."""
+    from oracle.torch_port import TorchCpuEncoder
+    cfg = synth.small_config()
+    img = synth.make_model(cfg, seed=17)
+    port = TorchCpuEncoder(img, cfg, threads=2)
+    ora = orc.OracleModel(img, cfg)
+    for L in (1, 37, 200):
+        ids = np.random.default_rng(L).integers(1, cfg["vocab_size"], size=L).astype(np.uint32)
+        a, b = port.forward(ids), ora.forward(ids)
+        assert a.shape == b.shape == (L, 128)
+        assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-5, L
+    ora.close()
