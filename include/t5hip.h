@@ -86,6 +86,20 @@ int t5h_encode_normalized(t5h_model* model, const uint32_t* ids, const int32_t* 
  * reported by t5h_synchronize. */
 int t5h_encode_device(t5h_model* model, const uint32_t* d_ids, const int32_t* cu_seqlens,
                       int32_t B, float* d_out, float* d_norm);
+
+/* No counterpart in the reference.  For callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): t5h_encode_device with the
+ * same arguments, ordering and results (bit-identical), but it allocates nothing -- no
+ * device, pinned or event allocation, per call or on first use.  Its workspace is a fixed
+ * array of T5H_NOALLOC_SCRATCH_BYTES per GPU, mapped by t5h_create and held by every GPU the
+ * library runs on until the process ends (about 2,000 tokens of XTR-base per call).  Inputs
+ * whose workspace does not fit return T5H_ERR_INVALID before anything is enqueued.  All calls
+ * on one GPU share that GPU's array: calls that overlap on one GPU (two handles on two
+ * streams, or two threads) race and must be serialised by the caller.  No per-kernel event
+ * timing is recorded for these calls. */
+#define T5H_NOALLOC_SCRATCH_BYTES (40u << 20)
+int t5h_encode_device_noalloc(t5h_model* model, const uint32_t* d_ids, const int32_t* cu_seqlens,
+                              int32_t B, float* d_out, float* d_norm);
 int t5h_synchronize(t5h_model* model);
 /* The model's hipStream_t (as void*), for event timing by the caller. */
 void* t5h_stream(t5h_model* model);

@@ -50,6 +50,7 @@ SIGNATURES = {
     "t5h_encode": (C.c_int, [_vp, _u32p, _i32p, C.c_int32, _f32p, _vp]),
     "t5h_encode_normalized": (C.c_int, [_vp, _u32p, _i32p, C.c_int32, _f32p, _vp]),
     "t5h_encode_device": (C.c_int, [_vp, _vp, _i32p, C.c_int32, _vp, _vp]),
+    "t5h_encode_device_noalloc": (C.c_int, [_vp, _vp, _i32p, C.c_int32, _vp, _vp]),
     "t5h_synchronize": (C.c_int, [_vp]),
     "t5h_stream": (C.c_void_p, [_vp]),
     "t5h_embed_ids": (C.c_int, [_vp, _u32p, C.c_int32, C.c_int32, C.c_int32, _f32p, _i32p,

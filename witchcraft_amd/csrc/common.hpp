@@ -165,6 +165,13 @@ hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int 
                            hipStream_t s);
 hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, int M, int N, int D, bool bf16_b,
                                 hipStream_t s);
+// Attention work items written from kernel arguments: CAP sequences per launch.
+struct WorkChunk {
+  static constexpr int CAP = 96;
+  int n;
+  int start[CAP], len[CAP], wofs[CAP];
+};
+hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s);
 hipError_t launch_window_sum(const float* win_out, const int* src_rows, int n_tokens, int max_windows,
                              int P, float* sum, float* norm, float* normalized, hipStream_t s);
 }  // namespace t5k

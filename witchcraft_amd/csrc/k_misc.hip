@@ -279,6 +279,15 @@ __global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict
   for (int i = lane; i < P; i += 64) normalized[(size_t)t * P + i] = sum[(size_t)t * P + i] / nv;
 }
 
+// Attention work list from by-value arguments (no host staging buffer): item wofs[i] + q of
+// sequence i is (start[i], len[i], 64 q, 0), the layout upload_batch writes.
+__global__ __launch_bounds__(256) void work_list_kernel(t5k::WorkChunk c, int4* __restrict__ work) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= c.n) return;
+  const int L = c.len[i];
+  for (int q = 0; q * 64 < L; q++) work[c.wofs[i] + q] = make_int4(c.start[i], L, q * 64, 0);
+}
+
 }  // namespace
 
 namespace t5k {
@@ -307,6 +316,12 @@ hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hi
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, K);
+  return hipGetLastError();
+}
+hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s) {
+  if (c.n <= 0) return hipSuccess;
+  if (c.n > WorkChunk::CAP) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(work_list_kernel, dim3((c.n + 255) / 256), dim3(256), 0, s, c, work);
   return hipGetLastError();
 }
 hipError_t launch_window_sum(const float* win, const int* src, int n, int maxw, int P, float* sum,

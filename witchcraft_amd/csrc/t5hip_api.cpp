@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <memory>
+#include <mutex>
 #include <stdlib.h>
 #include <string>
 #include <vector>
@@ -26,6 +27,34 @@ thread_local std::string g_err;
 int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
+}
+}  // namespace
+
+// The workspace of t5h_encode_device_noalloc: one fixed array per GPU the library runs on,
+// held until the process ends.  In host code `scratch` names only a host-side stand-in for
+// the symbol; each device's own address comes from hipGetSymbolAddress (scratch_init) and
+// is the only address that reaches kernels or copies.
+static __device__ __align__(256) uint8_t scratch[T5H_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Maps the scratch array on device `dev` (which must be current) once per process.
+int scratch_init(int dev, void** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  *out = nullptr;
+  if (dev < 0 || dev >= kMaxDevices) return fail(T5H_ERR_NODEVICE, "device index beyond the scratch table");
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(T5H_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return T5H_OK;
 }
 }  // namespace
 
@@ -74,6 +103,25 @@ const char* const kKernelNames[K_COUNT] = {
     "embed_gather", "rmsnorm", "gemm_qkv", "attention", "gemm_o", "gemm_ffn_gate_up",
     "gemm_ffn_wo", "gemm_proj", "rownorm"};
 
+// Per-forward device buffers, rows padded to tpad = roundup(T, 512) + 128.
+struct Workspace {
+  int tpad = 0;
+  float* x = nullptr;      // residual stream f32 [tpad][d_model]
+  _Float16* xn = nullptr;  // GEMM operand f16 [tpad][max(d_model, inner)], operand order
+  // Norm records of the folded T5LayerNorm (GemmArgs::rec), [tpad][16] f32 each on the batched
+  // path and [tpad][64] on the GEMV path: rec0 for the norm before attention and the final
+  // one, rec1 for the norm before the FFN.
+  float* rec0 = nullptr;
+  float* rec1 = nullptr;
+  _Float16* qkvb = nullptr;  // q/k/v f16 head-major [3][H][tpad][d_kv]
+  _Float16* ao = nullptr;    // attention output f16 [tpad][inner], operand order
+  _Float16* hb = nullptr;    // gated hidden state f16 [tpad][d_ff], operand order
+  float* out = nullptr;      // projections f32 [tpad][proj_dim]
+  float* norm = nullptr;     // their norms f32 [tpad]
+  uint32_t* ids = nullptr;   // token ids [tpad]
+  int4* work = nullptr;      // attention work list [cap_work]
+};
+
 struct StagingSlot {
   void* host = nullptr;  // pinned
   size_t cap = 0;
@@ -114,25 +162,14 @@ struct t5h_model {
   void* ws = nullptr;
   size_t ws_bytes = 0;
   int cap_tokens = 0, cap_seqs = 0, cap_work = 0;
-  int tpad = 0;
-  float* x = nullptr;
-  _Float16* xn = nullptr;
-  // Norm records of the folded T5LayerNorm (GemmArgs::rec), [tpad][16] f32 each on the batched
-  // path and [tpad][64] on the GEMV path: rec0 for the norm before attention and the final
-  // one, rec1 for the norm before the FFN.
-  float* rec0 = nullptr;
-  float* rec1 = nullptr;
-  _Float16* qkvb = nullptr;
-  _Float16* ao = nullptr;
-  _Float16* hb = nullptr;
-  float* out = nullptr;
-  float* norm = nullptr;
-  uint32_t* ids = nullptr;
-  int4* work = nullptr;
+  // The buffers every launch of a forward reads and writes: carved from `ws`, or from the
+  // library's fixed per-device array for t5h_encode_device_noalloc (swapped in for that call).
+  Workspace w;
   // Out-of-vocabulary flag in mapped pinned host memory: the embed kernel stores 1 through
   // err_flag (its device address); the host reads err_host after the stream is synchronised.
   unsigned* err_host = nullptr;
   unsigned* err_flag = nullptr;
+  void* scratch = nullptr;  // this device's address of the no-alloc scratch array
 
   // ---- host staging ----
   StagingSlot slots[4];
@@ -263,12 +300,13 @@ int add_f32_vector(HostArena& ha, const t5h::GgufFile& g, const std::string& nam
   return T5H_OK;
 }
 
-int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
-  if (T <= m->cap_tokens && B <= m->cap_seqs && nwork <= m->cap_work) return T5H_OK;
-  const int capT = std::max(T, m->cap_tokens), capB = std::max(B, m->cap_seqs);
-  const int capW = std::max(nwork, m->cap_work);
-  // GEMM tiles read A rows up to roundup(T, 512); attention reads up to T + 63.
-  const int tpad = (capT + 511) / 512 * 512 + 128;
+// Rows every workspace buffer holds for T tokens: GEMM tiles read A rows up to
+// roundup(T, 512); attention reads up to T + 63.
+int workspace_tpad(int T) { return (T + 511) / 512 * 512 + 128; }
+
+// Lays the workspace of tpad rows and capW attention work items out from `base` (nullptr:
+// only measure) and returns its size in bytes.
+size_t carve_workspace(const t5h_model* m, int tpad, int capW, uint8_t* base, Workspace& w) {
   const t5h_config& c = m->cfg;
   size_t off = 0;
   auto take = [&](size_t n) {
@@ -286,6 +324,30 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
   const size_t o_ids = take((size_t)tpad * 4);
   const size_t o_work = take((size_t)capW * sizeof(int4));
   const size_t o_rec = take((size_t)2 * tpad * NORM_REC_GEMV * 4);
+  if (base) {
+    w.tpad = tpad;
+    w.x = (float*)(base + o_x);
+    w.xn = (_Float16*)(base + o_xn);
+    w.qkvb = (_Float16*)(base + o_qkv);
+    w.ao = (_Float16*)(base + o_ao);
+    w.hb = (_Float16*)(base + o_hb);
+    w.out = (float*)(base + o_out);
+    w.norm = (float*)(base + o_norm);
+    w.ids = (uint32_t*)(base + o_ids);
+    w.work = (int4*)(base + o_work);
+    w.rec0 = (float*)(base + o_rec);
+    w.rec1 = w.rec0 + (size_t)tpad * NORM_REC_GEMV;
+  }
+  return off;
+}
+
+int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
+  if (T <= m->cap_tokens && B <= m->cap_seqs && nwork <= m->cap_work) return T5H_OK;
+  const int capT = std::max(T, m->cap_tokens), capB = std::max(B, m->cap_seqs);
+  const int capW = std::max(nwork, m->cap_work);
+  const int tpad = workspace_tpad(capT);
+  Workspace w;
+  const size_t off = carve_workspace(m, tpad, capW, nullptr, w);
   if (m->ws) {
     HIP_OK(hipStreamSynchronize(m->stream));
     HIP_OK(hipFree(m->ws));
@@ -297,20 +359,8 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
     return fail(T5H_ERR_NOMEM, "workspace allocation of " + std::to_string(off) + " bytes failed");
   }
   HIP_OK(hipMemset(m->ws, 0, off));
-  uint8_t* base = (uint8_t*)m->ws;
   m->ws_bytes = off;
-  m->tpad = tpad;
-  m->x = (float*)(base + o_x);
-  m->xn = (_Float16*)(base + o_xn);
-  m->qkvb = (_Float16*)(base + o_qkv);
-  m->ao = (_Float16*)(base + o_ao);
-  m->hb = (_Float16*)(base + o_hb);
-  m->out = (float*)(base + o_out);
-  m->norm = (float*)(base + o_norm);
-  m->ids = (uint32_t*)(base + o_ids);
-  m->work = (int4*)(base + o_work);
-  m->rec0 = (float*)(base + o_rec);
-  m->rec1 = m->rec0 + (size_t)tpad * NORM_REC_GEMV;
+  carve_workspace(m, tpad, capW, (uint8_t*)m->ws, m->w);
   m->cap_tokens = tpad - 128;
   m->cap_seqs = capB;
   m->cap_work = capW;
@@ -405,7 +455,7 @@ bool fold_norm(const t5h_model* m, int T) {
 // Floats per norm record: the GEMV kernels keep one partial sum per 16 columns.
 int rec_stride(const t5h_model* m, int T) { return use_gemv(m, T) ? NORM_REC_GEMV : 16; }
 
-// C = A . W^T (+ epilogue).  norm_w: on the GEMV path the operand is T5LayerNorm(m->x) with
+// C = A . W^T (+ epilogue).  norm_w: on the GEMV path the operand is T5LayerNorm(m->w.x) with
 // this weight, computed inside the kernel (A is then unused); callers pass it only when
 // use_gemv() holds.  nl: folded norm (fold_norm() holds), on either path.
 int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, const _Float16* A, int lda,
@@ -423,7 +473,7 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   a.n_off = n_off;
   a.heads = m->cfg.num_heads;
   a.dkv = m->cfg.d_kv;
-  a.tpad = m->tpad;
+  a.tpad = m->w.tpad;
   const double mats = W1 ? 2.0 : 1.0;
   const double flops = 2.0 * M * W.N * W.K * mats;
   const double out_bytes = (epi == EPI_F32 || epi == EPI_RESID ? 4.0 : 2.0) * M * W.N *
@@ -440,7 +490,7 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   }
   if (use_gemv(m, M)) {
     if (norm_w) {
-      a.xf = m->x;
+      a.xf = m->w.x;
       a.gamma = norm_w;
       a.eps = m->cfg.layer_norm_epsilon;
     }
@@ -490,7 +540,7 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
     const int L = cu[b + 1] - cu[b];
     for (int q = 0; q * 64 < L; q++) hw[w++] = make_int4(cu[b], L, q * 64, 0);
   }
-  if (nwork) HIP_OK(hipMemcpyAsync(m->work, hw, (size_t)nwork * sizeof(int4), hipMemcpyHostToDevice, m->stream));
+  if (nwork) HIP_OK(hipMemcpyAsync(m->w.work, hw, (size_t)nwork * sizeof(int4), hipMemcpyHostToDevice, m->stream));
   HIP_OK(hipEventRecord(s.done, m->stream));
   s.used = true;
   m->last_cu.assign(cu, cu + B + 1);
@@ -521,7 +571,7 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
   rc = T5H_OK;
   if (use_gemv(m, T)) return w;
   Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
-  const hipError_t e = t5k::launch_rmsnorm(m->x, w, m->xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon, m->stream);
+  const hipError_t e = t5k::launch_rmsnorm(m->w.x, w, m->w.xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon, m->stream);
   if (e != hipSuccess) rc = fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
   return nullptr;
 }
@@ -529,14 +579,14 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
 // T5LayerNorm of the residual stream in record mode, for GEMMs that fold the norm.
 int prenorm_rec(t5h_model* m, const float* w, int T) {
   Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
-  const hipError_t e = t5k::launch_rmsnorm(m->x, w, m->xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
-                                           m->stream, m->rec0, rec_stride(m, T));
+  const hipError_t e = t5k::launch_rmsnorm(m->w.x, w, m->w.xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
+                                           m->stream, m->w.rec0, rec_stride(m, T));
   if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
   return T5H_OK;
 }
 
 // One encoder block.  When the GEMMs fold the norms (fold_norm), the operand of the
-// block's first norm is either made here (operand_ready false) or was left in m->xn / rec0 by
+// block's first norm is either made here (operand_ready false) or was left in m->w.xn / rec0 by
 // the previous block's wo GEMM; with next_gamma set, this block's wo GEMM in turn prepares the
 // operand of the norm that follows (next block's first norm or the final one).
 int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
@@ -551,15 +601,15 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
   const NormLink* qkv_nl = nullptr;
   if (fold) {
     if (!operand_ready && (rc = prenorm_rec(m, Ly.ln0, T))) return rc;
-    qn.rec = m->rec0;
-    qn.rec_next = m->rec1;
-    on.rec = m->rec1;
-    on.nx = m->xn;
+    qn.rec = m->w.rec0;
+    qn.rec_next = m->w.rec1;
+    on.rec = m->w.rec1;
+    on.nx = m->w.xn;
     on.ngamma = Ly.ln1;
-    fn.rec = m->rec1;
-    fn.rec_next = m->rec0;
-    wn.rec = m->rec0;
-    wn.nx = m->xn;
+    fn.rec = m->w.rec1;
+    fn.rec_next = m->w.rec0;
+    wn.rec = m->w.rec0;
+    wn.nx = m->w.xn;
     wn.ngamma = next_gamma;
     qkv_nl = &qn;
   } else {
@@ -567,26 +617,26 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     if (rc) return rc;
   }
   if (Ly.fused_qkv) {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0, qkv_nl))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.qkv, nullptr, m->w.xn, D, T, m->w.qkvb, 0, 0, nw0, qkv_nl))) return rc;
   } else {
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->xn, D, T, m->qkvb, 0, 0, nw0, qkv_nl))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->xn, D, T, m->qkvb, 0, inner, nw0, qkv_nl))) return rc;
-    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->xn, D, T, m->qkvb, 0, 2 * inner, nw0, qkv_nl)))
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.q, nullptr, m->w.xn, D, T, m->w.qkvb, 0, 0, nw0, qkv_nl))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.k, nullptr, m->w.xn, D, T, m->w.qkvb, 0, inner, nw0, qkv_nl))) return rc;
+    if ((rc = gemm(m, K_GEMM_QKV, EPI_QKV, Ly.v, nullptr, m->w.xn, D, T, m->w.qkvb, 0, 2 * inner, nw0, qkv_nl)))
       return rc;
   }
   {
     AttnArgs a{};
-    a.qkv = m->qkvb;
-    a.out = m->ao;
-    a.work = m->work;
+    a.qkv = m->w.qkvb;
+    a.out = m->w.ao;
+    a.work = m->w.work;
     a.lut = m->rel_lut;
     a.heads = c.num_heads;
-    a.tpad = m->tpad;
+    a.tpad = m->w.tpad;
     a.lutw = m->lutw;
     Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
   }
-  if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->ao, inner, T, m->x, D, 0, nullptr, fold ? &on : nullptr)))
+  if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->w.ao, inner, T, m->w.x, D, 0, nullptr, fold ? &on : nullptr)))
     return rc;
   const float* nw1 = nullptr;
   if (!fold) {
@@ -595,32 +645,43 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
   }
   const NormLink* ffn_nl = fold ? &fn : nullptr;
   if (c.feed_forward_gated) {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, D, T, m->hb, c.d_ff, 0, nw1, ffn_nl)))
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn, D, T, m->w.hb, c.d_ff, 0, nw1, ffn_nl)))
       return rc;
   } else {
-    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->xn, D, T, m->hb, c.d_ff, 0, nw1, ffn_nl)))
+    if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_RELU, Ly.wi0, nullptr, m->w.xn, D, T, m->w.hb, c.d_ff, 0, nw1, ffn_nl)))
       return rc;
   }
-  if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, D, 0, nullptr,
+  if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, D, 0, nullptr,
                  fold && next_gamma ? &wn : nullptr)))
     return rc;
   return T5H_OK;
 }
 
-// Full forward from device ids; results in m->out / m->norm (or the given pointers).
+// Full forward from device ids; results in m->w.out / m->w.norm (or the given pointers).
+int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* d_out, float* d_norm,
+                  int normalize);
+
 int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
                     float* d_norm, int normalize) {
   int nwork = 0, rc;
   if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
   if ((rc = upload_batch(m, cu, B, nwork))) return rc;
+  return enqueue_stack(m, d_ids, T, nwork, d_out, d_norm, normalize);
+}
+
+// The launches of one forward on the workspace m->w, whose attention work list (nwork items)
+// is in place.
+int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* d_out, float* d_norm,
+                  int normalize) {
+  int rc;
   const t5h_config& c = m->cfg;
   // With folded norms the embedding gather also emits the first norm's operand and records.
   const bool fold = fold_norm(m, T);
   {
     Timed t(m, K_EMBED, 0, (double)T * c.d_model * 8);
     const float* g0 = c.num_layers > 0 ? m->layers[0].ln0 : m->final_ln;
-    HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->x, m->err_flag, m->stream,
-                             g0, c.layer_norm_epsilon, fold ? m->xn : nullptr, fold ? m->rec0 : nullptr,
+    HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->w.x, m->err_flag, m->stream,
+                             g0, c.layer_norm_epsilon, fold ? m->w.xn : nullptr, fold ? m->w.rec0 : nullptr,
                              rec_stride(m, T)));
   }
   for (int l = 0; l < c.num_layers; l++) {
@@ -630,12 +691,12 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
   const float* nwf = nullptr;
   NormLink pn;
   if (fold) {
-    pn.rec = m->rec0;
+    pn.rec = m->w.rec0;
   } else {
     nwf = prenorm(m, m->final_ln, T, rc);
     if (rc) return rc;
   }
-  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->xn, c.d_model, T, d_out, c.proj_dim, 0, nwf,
+  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->w.xn, c.d_model, T, d_out, c.proj_dim, 0, nwf,
                  fold ? &pn : nullptr)))
     return rc;
   {
@@ -649,6 +710,62 @@ int check_model(t5h_model* m) {
   if (!m) return fail(T5H_ERR_INVALID, "model handle is NULL");
   HIP_OK(hipSetDevice(m->device));
   return T5H_OK;
+}
+
+// t5h_encode_device on the device's fixed scratch array: no device or host allocation.  The
+// workspace is carved from the array and the attention work list is written by a kernel from
+// its arguments.  Nothing needs clearing between calls: every buffer is written before it is
+// read, except rows past the last token, which only feed outputs that are never stored (the
+// attention kernel zeroes value rows past a sequence's end as it loads them).
+int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, float* d_out,
+                          float* d_norm) {
+  int rc, T = 0;
+  if ((rc = check_model(m))) return rc;
+  if ((rc = validate_cu(m, cu, B, T))) return rc;
+  if (T == 0) return T5H_OK;
+  if (!d_ids || !d_out) return fail(T5H_ERR_INVALID, "d_ids/d_out must not be NULL");
+  if (!m->scratch) return fail(T5H_ERR_HIP, "no-alloc scratch array is not mapped on this device");
+  int nwork = 0;
+  for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
+  const int tpad = workspace_tpad(T);
+  Workspace w;
+  const size_t need = carve_workspace(m, tpad, nwork, nullptr, w);
+  if (need > (size_t)T5H_NOALLOC_SCRATCH_BYTES)
+    return fail(T5H_ERR_INVALID, "no-alloc encode of " + std::to_string(T) + " tokens needs " +
+                                     std::to_string(need) + " bytes of workspace; the fixed scratch array holds " +
+                                     std::to_string((size_t)T5H_NOALLOC_SCRATCH_BYTES));
+  carve_workspace(m, tpad, nwork, (uint8_t*)m->scratch, w);
+  // Work list in the order upload_batch uses (longest sequences first); m->order is the
+  // handle's host scratch, reused across calls.
+  m->order.resize(B);
+  for (int b = 0; b < B; b++) m->order[b] = b;
+  std::stable_sort(m->order.begin(), m->order.end(),
+                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+  t5k::WorkChunk ch;
+  ch.n = 0;
+  int wofs = 0;
+  for (int i = 0; i < B; i++) {
+    const int b = m->order[i], L = cu[b + 1] - cu[b];
+    if (L == 0) continue;
+    ch.start[ch.n] = cu[b];
+    ch.len[ch.n] = L;
+    ch.wofs[ch.n] = wofs;
+    wofs += (L + 63) / 64;
+    if (++ch.n == t5k::WorkChunk::CAP) {
+      HIP_OK(t5k::launch_work_list(ch, w.work, m->stream));
+      ch.n = 0;
+    }
+  }
+  HIP_OK(t5k::launch_work_list(ch, w.work, m->stream));
+  // Run the stack on the scratch workspace without event timing (events would be created).
+  const Workspace saved = m->w;
+  const bool prof = m->prof;
+  m->w = w;
+  m->prof = false;
+  rc = enqueue_stack(m, d_ids, T, nwork, d_out, d_norm, 0);
+  m->w = saved;
+  m->prof = prof;
+  return rc;
 }
 
 int finish_sync(t5h_model* m) {
@@ -678,10 +795,10 @@ int encode_host(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B,
   if ((rc = ensure_io(m, ids_b + out_b + norm_b))) return rc;
   uint8_t* io = (uint8_t*)m->io;
   memcpy(io, ids, (size_t)T * 4);
-  HIP_OK(hipMemcpyAsync(m->ids, io, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
-  if ((rc = enqueue_forward(m, m->ids, cu, B, T, m->out, m->norm, normalize))) return rc;
-  HIP_OK(hipMemcpyAsync(io + ids_b, m->out, out_b, hipMemcpyDeviceToHost, m->stream));
-  HIP_OK(hipMemcpyAsync(io + ids_b + out_b, m->norm, norm_b, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(m->w.ids, io, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
+  if ((rc = enqueue_forward(m, m->w.ids, cu, B, T, m->w.out, m->w.norm, normalize))) return rc;
+  HIP_OK(hipMemcpyAsync(io + ids_b, m->w.out, out_b, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(io + ids_b + out_b, m->w.norm, norm_b, hipMemcpyDeviceToHost, m->stream));
   if ((rc = finish_sync(m))) return rc;
   memcpy(out, io + ids_b, out_b);
   if (out_norm) memcpy(out_norm, io + ids_b + out_b, norm_b);
@@ -707,8 +824,11 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(T5H_ERR_NODEVICE, std::string("t5-hip kernels target gfx950, device is ") + prop.gcnArchName);
   HIP_OK(hipSetDevice(dev));
+  void* scratch_dev = nullptr;
+  if ((rc = scratch_init(dev, &scratch_dev))) return rc;
 
   std::unique_ptr<t5h_model> m(new t5h_model());
+  m->scratch = scratch_dev;
   m->cfg = *cfg;
   m->device = dev;
   m->inner = cfg->num_heads * cfg->d_kv;
@@ -931,6 +1051,11 @@ int t5h_encode_device(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, in
   return enqueue_forward(m, d_ids, cu, B, T, d_out, d_norm, 0);
 }
 
+int t5h_encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int32_t B, float* d_out,
+                              float* d_norm) {
+  return encode_device_noalloc(m, d_ids, cu, B, d_out, d_norm);
+}
+
 int t5h_synchronize(t5h_model* m) {
   int rc;
   if ((rc = check_model(m))) return rc;
@@ -1070,9 +1195,9 @@ int t5h_layer_forward(t5h_model* m, int32_t layer, const float* x_in, const int3
   int nwork = 0;
   if ((rc = upload_batch(m, cu, B, nwork))) return rc;
   const size_t bytes = (size_t)T * m->cfg.d_model * 4;
-  HIP_OK(hipMemcpyAsync(m->x, x_in, bytes, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(hipMemcpyAsync(m->w.x, x_in, bytes, hipMemcpyHostToDevice, m->stream));
   if ((rc = run_block(m, layer, T, nwork))) return rc;
-  HIP_OK(hipMemcpyAsync(x_out, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(x_out, m->w.x, bytes, hipMemcpyDeviceToHost, m->stream));
   return finish_sync(m);
 }
 
@@ -1087,14 +1212,14 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   const t5h_config& c = m->cfg;
   const Layer& Ly = m->layers[layer];
   const size_t bytes = (size_t)T * c.d_model * 4;
-  HIP_OK(hipMemcpyAsync(m->x, x, bytes, hipMemcpyHostToDevice, m->stream));
-  HIP_OK(t5k::launch_f32_to_f16(m->x, m->xn, (size_t)T * c.d_model, c.d_model, m->stream));
+  HIP_OK(hipMemcpyAsync(m->w.x, x, bytes, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(t5k::launch_f32_to_f16(m->w.x, m->w.xn, (size_t)T * c.d_model, c.d_model, m->stream));
   m->batched_only = mode == 1;
-  rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->xn, c.d_model, T, m->hb, c.d_ff);
-  if (!rc) rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->hb, c.d_ff, T, m->x, c.d_model);
+  rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn, c.d_model, T, m->w.hb, c.d_ff);
+  if (!rc) rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, c.d_model);
   m->batched_only = false;
   if (rc) return rc;
-  HIP_OK(hipMemcpyAsync(y, m->x, bytes, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(y, m->w.x, bytes, hipMemcpyDeviceToHost, m->stream));
   return finish_sync(m);
 }
 

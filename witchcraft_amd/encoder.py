@@ -114,6 +114,12 @@ class T5EncoderModel:
         check(lib.t5h_encode_device(self._h, C.c_void_p(d_ids), cu, cu.size - 1, C.c_void_p(d_out),
                                     C.c_void_p(d_norm) if d_norm else None))
 
+    def encode_device_noalloc(self, d_ids: int, cu_seqlens: np.ndarray, d_out: int, d_norm: int | None = None):
+        """encode_device on the library's fixed per-GPU scratch array: allocates nothing."""
+        cu = np.ascontiguousarray(cu_seqlens, np.int32)
+        check(lib.t5h_encode_device_noalloc(self._h, C.c_void_p(d_ids), cu, cu.size - 1, C.c_void_p(d_out),
+                                            C.c_void_p(d_norm) if d_norm else None))
+
     def synchronize(self) -> None:
         check(lib.t5h_synchronize(self._h))
 
