@@ -8,10 +8,13 @@ HBM.  Default workload: cfg2, 32 sequences padded to 256 with true lengths U[32,
 Prints ONE JSON line.  Extra fields:
   roofline      -- the dominant kernel (batched FFN gate/up dequant-GEMM) vs f16 MFMA peak,
                    timed with HIP events on the model's stream inside this process;
-  cpu_baseline  -- the CPU oracle (a C restatement of the reference's default t5-quantized
-                   CPU path: Q4_K dequantized to f32 at load, f32 GEMMs) on a bounded sample
-                   of the same workload, batch-1 per sequence as the reference runs it;
-  kernels       -- per-kernel-class averages from the same event timing.
+  cpu_baseline  -- restatements of the reference's CPU encoder (oracle/: the default
+                   t5-quantized f32 path on torch CPU GEMMs and in C, and the x86 default
+                   hybrid-dequant + fbgemm numerics in C) on a bounded sample of the same
+                   workload, batch-1 per sequence as the reference runs it;
+  kernels       -- per-kernel-class averages from the same event timing;
+  query         -- (cfg2) the cfg3 query regime: p50 / p95 latency over 1,000 queries cycling
+                   8 model replicas, and its dominant GEMV against the HBM roofline.
 """
 from __future__ import annotations
 
@@ -44,54 +47,134 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_s: float) -> dict:
-    """Oracle (port of the reference CPU path) timed per sequence: 1 warmup + median of 7
-    (tools/t5-bench/src/main.rs:44-69), over as many sequences as fit the time budget."""
-    from oracle import oracle as orc
+def cpu_info() -> dict:
+    """The host the CPU baseline runs on: model name, logical CPUs, CPUs this process may run
+    on, and the thread count it uses (the box's CPU share: OMP_NUM_THREADS when set)."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or affinity
+    return {"model": model, "nproc": os.cpu_count(), "affinity": affinity, "threads": min(share, affinity)}
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    m = orc.OracleModel(img, cfg)
+
+def _time_per_sequence(fn, ids, cu, budget_s: float):
+    """The reference harness's protocol (tools/t5-bench/src/main.rs:44-69), batch-1 per
+    sequence: 1 warmup + median of 7, over as many sequences as fit the budget.
+    Returns (tokens, seconds, sequences)."""
     tok, secs, used = 0, 0.0, 0
     t_start = time.perf_counter()
     for b in range(cu.size - 1):
         seq = ids[cu[b]:cu[b + 1]]
-        m.forward(seq, acc64=False)
+        fn(seq)
         times = []
         for _ in range(7):
             t = time.perf_counter()
-            m.forward(seq, acc64=False)
+            fn(seq)
             times.append(time.perf_counter() - t)
         tok += seq.size
         secs += sorted(times)[3]
         used += 1
         if time.perf_counter() - t_start > budget_s:
             break
-    m.close()
-    cpu = "unknown"
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": tok / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{used} of {cu.size - 1} sequences ({tok} tokens), batch-1 each, "
-                      f"median of 7 after 1 warmup; f32 dequantize-at-load path; CPU: {cpu}"}
+    return tok, secs, used
 
 
-def query_bench(args) -> None:
-    """cfg3 (query regime): B = 1, L = 32 tokens, one forward per query, latency p50/p95 over
-    `--queries` queries (>= 1000).  With --rotate R (default 8) the
-    queries cycle over R independent model replicas (R x 47.8 MB of Q4_K weights > the 256 MB
-    MALL), so weights stream from HBM as in a cold query; --rotate 1 measures the warm case."""
+def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_s: float) -> dict:
+    """The reference's CPU encoder numerics timed on this host, per sequence as the reference
+    runs them.  Three restatements (test infrastructure under oracle/):
+      f32_torch     -- the default t5-quantized path (Q4_K dequantized to f32 at load, f32 GEMMs,
+                       src/quantized_t5.rs:39-49) on torch's multithreaded CPU GEMMs: the
+                       strong-BLAS figure, reported as `value`;
+      f32_c         -- the same path in the C oracle's loops (OpenMP over output rows);
+      hybrid_bf16_c -- the x86 default build (hybrid-dequant + fbgemm, Makefile:26-30): Q8_K x
+                       Q4_K integer dots for wi_0/wi_1/linear with the Pade gelu, bf16-truncated
+                       q/k/v/o/wo (src/fused_matmul.rs:138-177, fbgemm-rs/src/bf16.rs:21-25),
+                       in the C oracle's scalar loops (no fbgemm assembly kernels).
+    The value is the fastest variant, so the GPU/CPU ratio is the least flattering one."""
+    from oracle import oracle as orc
+    from oracle.torch_port import TorchCpuEncoder
+
+    info = cpu_info()
+    threads = info["threads"]
+    used_omp = orc.set_threads(threads)
+    variants = {}
+    share = budget_s / 3
+    port = TorchCpuEncoder(img, cfg, threads=threads)
+    tok, secs, n = _time_per_sequence(port.forward, ids, cu, share)
+    variants["f32_torch"] = {"tokens_per_s": tok / secs, "sequences": n, "tokens": tok, "threads": threads}
+    del port
+    for name, var in (("f32_c", orc.VARIANT_DEFAULT), ("hybrid_bf16_c", orc.VARIANT_HYBRID_BF16)):
+        m = orc.OracleModel(img, cfg, variant=var)
+        tok, secs, n = _time_per_sequence(lambda s: m.forward(s, acc64=False), ids, cu, share)
+        m.close()
+        variants[name] = {"tokens_per_s": tok / secs, "sequences": n, "tokens": tok, "threads": used_omp}
+    best = max(variants, key=lambda k: variants[k]["tokens_per_s"])
+    v = variants[best]
+    return {"value": v["tokens_per_s"], "unit": "tokens/s", "cores": v["threads"], "kind": "port",
+            "sample": f"{best}: {v['sequences']} of {cu.size - 1} sequences ({v['tokens']} tokens), batch-1 each, "
+                      f"median of 7 after 1 warmup; CPU {info['model']}, nproc {info['nproc']}, "
+                      f"{info['affinity']} CPUs in this process's affinity, {threads} threads "
+                      f"(this GPU box's CPU share)",
+            "cpu": info, "variants": variants}
+
+
+def kernel_table(model, step, n: int, reps: int = 20, unit: str = "step") -> dict:
+    """Per kernel class: launches per step, and the average launch duration from `reps`
+    back-to-back relaunches of the class's last launch in a profiled forward, between two HIP
+    events on the model's stream (t5h_replay_kernel).  event_avg_us is the same class timed by
+    events around every launch inside the forwards, which adds each launch's dispatch and
+    completion latency; the relaunch figure is the one comparable with rocprofv3's
+    per-dispatch durations.  Algorithmic FLOP and bytes per launch come from the library."""
+    model.set_profiling(True)
+    for _ in range(n):
+        step()
+    model.synchronize()
+    stats = model.kernel_stats()
+    out = {}
+    for name, s in stats.items():
+        if not s["launches"]:
+            continue
+        us = model.replay_kernel(s["kind"], reps)
+        per = s["launches"] / n
+        k = {f"launches_per_{unit}": per, "avg_us": us, "ms_per_step": us * per * 1e-3,
+             "event_avg_us": s["total_ms"] / s["launches"] * 1e3}
+        if s["flops"]:
+            k["flops_per_launch"] = s["flops"] / s["launches"]
+            k["tflops"] = k["flops_per_launch"] / (us * 1e-6) / 1e12
+            k["mfma_frac"] = k["tflops"] / PEAK_F16_TFLOPS
+        if s["bytes"]:
+            k["bytes_per_launch"] = s["bytes"] / s["launches"]
+            k["gbs"] = k["bytes_per_launch"] / (us * 1e-6) / 1e9
+            k["hbm_frac"] = k["gbs"] / PEAK_HBM_GBS
+        out[name] = k
+    model.set_profiling(False)
+    return out
+
+
+QUERY_BYTES = 47_947_392  # cfg3 per query: Q4_K weights + embedding rows + bias table + output + ids
+
+
+def run_query(args, img: bytes | None = None, cpu: bool = True) -> dict:
+    """cfg3 (query regime): B = 1, L = 32 tokens, one forward per query from HBM-resident ids,
+    latency p50/p95 over `--queries` queries (>= 1000).  The queries cycle over `--rotate`
+    independent model replicas (default 8: 8 x 47.8 MB of Q4_K weights > the 256 MB MALL), so
+    weights stream from HBM as in a cold query; --rotate 1 measures the warm case.  Also the
+    dominant GEMV class from HIP events on the model's stream (one replica) against the HBM
+    roofline, and the CPU port's latency for the same queries."""
     import torch
 
     from witchcraft_amd import synth
     from witchcraft_amd.encoder import T5EncoderModel
 
     cfg = dict(synth.XTR_BASE)
-    img = synth.make_model(cfg, seed=args.seed)
+    if img is None:
+        img = synth.make_model(cfg, seed=args.seed)
     models = [T5EncoderModel.from_gguf(img, cfg, hip_device=0) for _ in range(args.rotate)]
     L = 32
     rng = np.random.default_rng(2000 + args.seed)
@@ -120,57 +203,60 @@ def query_bench(args) -> None:
     p50, p95 = float(np.percentile(lat, 50) * 1e6), float(np.percentile(lat, 95) * 1e6)
     log(f"[bench] cfg3: {args.queries} queries over {len(models)} replicas: p50 {p50:.1f} us, p95 {p95:.1f} us")
 
-    # per-kernel event timing (one replica, warm) -> dominant GEMV kernel vs HBM roofline
-    m = models[0]
-    m.set_profiling(True)
-    reps = 50
-    for i in range(reps):
-        query(0)
-    stats = m.kernel_stats()
-    m.set_profiling(False)
-    kernels = {}
-    for name, st in stats.items():
-        if st["launches"]:
-            kernels[name] = {"launches_per_query": st["launches"] / reps,
-                             "avg_us": st["total_ms"] / st["launches"] * 1e3}
-    gemv = {k: v for k, v in stats.items() if k.startswith("gemm_") and v["launches"]}
-    dom_name = max(gemv, key=lambda k: gemv[k]["total_ms"])
+    # per-kernel durations (one replica) -> dominant GEMV class vs the HBM roofline.  The
+    # relaunches of one kernel read its weights from the MALL after the first, so these are
+    # warm-cache figures; the latency above is the cold (rotated) one.
+    kernels = kernel_table(models[0], lambda: query(0), 20, unit="query")
+    for mm in models:
+        mm.close()
+    gemv = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
+    dom_name = max(gemv, key=lambda k: gemv[k]["ms_per_step"])
     dom = gemv[dom_name]
-    avg_s = dom["total_ms"] / dom["launches"] * 1e-3
-    bytes_per_launch = dom["bytes"] / dom["launches"]
+    avg_s = dom["avg_us"] * 1e-6
+    bytes_per_launch = dom["bytes_per_launch"]
     achieved = bytes_per_launch / avg_s / 1e9
-    q_bytes = 47_947_392  # Q4_K weights + embedding rows + bias table + output + ids per query
-    base = None
-    if not args.no_cpu_baseline:
-        from oracle import oracle as orc
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-        om = orc.OracleModel(img, cfg)
-        om.forward(pool[0].astype(np.uint32), acc64=False)
+    res = {"workload": "cfg3: XTR-base Q4_K encoder, query regime: batch 1, 32 tokens",
+           "p50_us": p50, "p95_us": p95, "queries": args.queries, "replicas_rotated": len(models),
+           "queries_per_s": args.queries / wall,
+           "query_bytes": QUERY_BYTES, "query_floor_us": QUERY_BYTES / PEAK_HBM_GBS / 1e3,
+           "whole_query_hbm_frac": QUERY_BYTES / (p50 * 1e-6) / 1e9 / PEAK_HBM_GBS,
+           "roofline": {"kernel": f"{dom_name} (Q4_K GEMV, M = 32)", "bound": "hbm", "achieved": achieved,
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+                        "traffic": None, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
+           "kernels": kernels, "cpu_baseline": None}
+    if cpu and not args.no_cpu_baseline:
+        from oracle.torch_port import TorchCpuEncoder
+        info = cpu_info()
+        port = TorchCpuEncoder(img, cfg, threads=info["threads"])
+        port.forward(pool[0])
         times = []
         t0 = time.perf_counter()
         for i in range(64):
             t = time.perf_counter()
-            om.forward(pool[i].astype(np.uint32), acc64=False)
+            port.forward(pool[i])
             times.append(time.perf_counter() - t)
-            if time.perf_counter() - t0 > args.cpu_budget:
+            if time.perf_counter() - t0 > min(args.cpu_budget, 5.0):
                 break
-        om.close()
-        med = sorted(times)[len(times) // 2]
-        base = {"value": med * 1e6, "unit": "us/query (p50)", "cores": threads, "kind": "port",
-                "sample": f"{len(times)} queries of 32 tokens, batch-1, f32 dequantize-at-load path"}
+        res["cpu_baseline"] = {"value": float(np.percentile(times, 50) * 1e6), "unit": "us/query (p50)",
+                               "cores": info["threads"], "kind": "port",
+                               "sample": f"{len(times)} queries of 32 tokens, batch-1, f32 dequantize-at-load "
+                                         f"path on torch CPU GEMMs; CPU {info['model']}"}
+    return res
+
+
+def query_bench(args) -> None:
+    """cfg3 as its own line: value = p50 latency per query."""
+    q = run_query(args)
     line = {
-        "metric": "XTR-base Q4_K query encode latency p50 (B=1, L=32)", "value": p50, "unit": "us",
-        "n_gpus": 1, "steps": args.queries, "warmup": args.warmup, "ms_per_step": p50 * 1e-3,
+        "metric": "XTR-base Q4_K query encode latency p50 (B=1, L=32)", "value": q["p50_us"], "unit": "us",
+        "n_gpus": 1, "steps": args.queries, "warmup": args.warmup, "ms_per_step": q["p50_us"] * 1e-3,
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "cfg3: XTR-base Q4_K encoder, query regime: batch 1, 32 tokens",
-                   "global_batch": 1, "seq_len": L, "replicas_rotated": len(models),
-                   "p95_us": p95, "queries_per_s": args.queries / wall, "parallelism": "single GPU"},
-        "roofline": {"kernel": f"{dom_name} (Q4_K GEMV, M = 32)", "bound": "hbm", "achieved": achieved,
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                     "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6,
-                     "query_bytes": q_bytes, "query_floor_us": q_bytes / PEAK_HBM_GBS / 1e3},
-        "cpu_baseline": base, "kernels": kernels,
+        "config": {"workload": q["workload"], "global_batch": 1, "seq_len": 32,
+                   "replicas_rotated": q["replicas_rotated"], "p95_us": q["p95_us"],
+                   "queries_per_s": q["queries_per_s"], "parallelism": "single GPU"},
+        "roofline": q["roofline"], "cpu_baseline": q["cpu_baseline"], "kernels": q["kernels"],
+        "query_bytes": q["query_bytes"], "query_floor_us": q["query_floor_us"],
     }
     print(json.dumps(line), flush=True)
 
@@ -295,7 +381,7 @@ def score_bench(args) -> None:
     base = None
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        threads = orc.set_threads(cpu_info()["threads"])
         r = np.random.default_rng(args.seed)
         ns = 1 << 17
         qa = r.standard_normal((M, D)).astype(np.float32)
@@ -405,6 +491,7 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--queries", type=int, default=1000, help="cfg3: number of timed queries")
     ap.add_argument("--rotate", type=int, default=8, help="cfg3: model replicas cycled (MALL defeat)")
+    ap.add_argument("--no-query", action="store_true", help="cfg2: leave out the cfg3 query object")
     ap.add_argument("--score-n", type=int, default=1 << 20, help="score: residual rows")
     ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
     ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
@@ -477,50 +564,48 @@ def main() -> None:
     value = T * args.steps / elapsed
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
 
-    # ---- per-kernel timing with HIP events on the model stream ----
-    model.set_profiling(True)
-    for _ in range(args.steps):
-        step()
-    model.synchronize()
-    stats = model.kernel_stats()
-    model.set_profiling(False)
-    kernels = {}
-    for name, s in stats.items():
-        if not s["launches"]:
-            continue
-        avg_ms = s["total_ms"] / s["launches"]
-        k = {"launches_per_step": s["launches"] / args.steps, "avg_us": avg_ms * 1e3,
-             "ms_per_step": s["total_ms"] / args.steps}
-        if s["flops"]:
-            k["tflops"] = s["flops"] / (s["total_ms"] * 1e-3) / 1e12
-            k["mfma_frac"] = k["tflops"] / PEAK_F16_TFLOPS
-        if s["bytes"]:
-            k["gbs"] = s["bytes"] / (s["total_ms"] * 1e-3) / 1e9
-            k["hbm_frac"] = k["gbs"] / PEAK_HBM_GBS
-        kernels[name] = k
+    # ---- per-kernel durations with HIP events on the model stream ----
+    kernels = kernel_table(model, step, args.steps)
     # dominant kernel = the GEMM class with the largest share of the step
-    gemms = {k: v for k, v in stats.items() if k.startswith("gemm_") and v["launches"]}
-    dom_name = max(gemms, key=lambda k: gemms[k]["total_ms"])
+    gemms = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
+    dom_name = max(gemms, key=lambda k: gemms[k]["ms_per_step"])
     dom = gemms[dom_name]
-    avg_s = dom["total_ms"] / dom["launches"] * 1e-3
-    flops_per_launch = dom["flops"] / dom["launches"]
+    avg_s = dom["avg_us"] * 1e-6
+    flops_per_launch = dom["flops_per_launch"]
     achieved = flops_per_launch / avg_s / 1e12
     traffic = None
+    counters = None
     tfile = ROOT / "profiles" / "encoder_cfg2_traffic.json"
     if args.workload == "cfg2" and args.seed == 0 and tfile.exists():
-        t = json.loads(tfile.read_text())["bytes_per_dispatch"].get(dom_name)
+        tj = json.loads(tfile.read_text())
+        t = tj["bytes_per_dispatch"].get(dom_name)
         traffic = t["fetch"] + t["write"] if t else None
+        c = tj.get("counters_gate_up")
+        if c and dom_name == "gemm_ffn_gate_up":
+            # MFMA work the counters saw this launch execute (instructions x 16x16x32 x 2),
+            # over the launch duration measured here
+            counters = {"mfma_flop_executed": c["mfma_flop_executed"],
+                        "tflops_executed": c["mfma_flop_executed"] / avg_s / 1e12,
+                        "frac_executed": c["mfma_flop_executed"] / avg_s / 1e12 / PEAK_F16_TFLOPS,
+                        "mfma_busy_frac": c["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * c["GRBM_GUI_ACTIVE"] / 8),
+                        "source": "profiles/encoder_cfg2_kernel_stats.md (rocprofv3 --pmc through bench.py)"}
     roofline = {"kernel": f"{dom_name} (Q4_K dequant-GEMM, v_mfma_f32_16x16x32_f16)",
                 "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
                 "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6,
-                "share_of_step": dom["total_ms"] / sum(v["total_ms"] for v in stats.values())}
+                "share_of_step": dom["ms_per_step"] / sum(v["ms_per_step"] for v in kernels.values()),
+                "counters": counters}
 
     base = None
     if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (oracle port, bounded sample) ...")
+        log("[bench] CPU baseline (ports of the reference CPU path, bounded sample) ...")
         base = cpu_baseline(img, cfg, ids, cu, args.cpu_budget)
-        log(f"[bench] CPU baseline {base['value']:.1f} tokens/s on {base['cores']} threads")
+        per = ", ".join(f"{k} {v['tokens_per_s']:.0f}" for k, v in base["variants"].items())
+        log(f"[bench] CPU baseline {base['value']:.1f} tokens/s on {base['cores']} threads ({per})")
+    query = None
+    if args.workload == "cfg2" and not args.no_query:
+        model.close()
+        query = run_query(args, img if args.seed == 0 else None)
 
     line = {
         "metric": METRIC, "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -531,6 +616,8 @@ def main() -> None:
                    "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": base, "kernels": kernels,
     }
+    if query is not None:
+        line["query"] = query
     print(json.dumps(line), flush=True)
 
 

@@ -221,6 +221,15 @@ typedef struct t5h_kernel_stat {
 } t5h_kernel_stat;
 int t5h_set_profiling(t5h_model* model, int32_t on);
 int t5h_kernel_stats(t5h_model* model, t5h_kernel_stat* stats, int32_t cap);
+/* Measurement hook (no reference counterpart): relaunches the last launch of kernel class
+ * `kind` (the index of its t5h_kernel_stats record) from the most recent forward run with
+ * profiling on, `reps` times back to back between two HIP events on the model's stream, and
+ * returns the average duration in microseconds.  Per-kernel events inside a forward add the
+ * dispatch and completion latency of every launch; back-to-back relaunches do not, so these
+ * averages are comparable with profiler per-dispatch durations.  The relaunches overwrite the
+ * workspace (a residual class adds into the residual stream again); the next forward
+ * recomputes it. */
+int t5h_replay_kernel(t5h_model* model, int32_t kind, int32_t reps, double* avg_us);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,7 @@ SIGNATURES = {
     "t5h_ffn_block": (C.c_int, [_vp, C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32]),
     "t5h_set_profiling": (C.c_int, [_vp, C.c_int32]),
     "t5h_kernel_stats": (C.c_int, [_vp, C.POINTER(T5HKernelStat), C.c_int32]),
+    "t5h_replay_kernel": (C.c_int, [_vp, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
 }
 
 

@@ -122,6 +122,27 @@ struct Workspace {
   int4* work = nullptr;      // attention work list [cap_work]
 };
 
+// The arguments of the last launch of each kernel class in a profiled forward, so that
+// t5h_replay_kernel can relaunch it back to back between two events.
+struct ReplayRec {
+  enum Type { NONE, GEMM, GEMV, ATTN, EMBED, ROWNORM, RMSNORM } type = NONE;
+  int epi = 0, wfmt = 0, n = 0;
+  GemmArgs ga{};
+  t5k::GemmPlan plan{};
+  AttnArgs aa{};
+  // embed / rownorm / rmsnorm
+  const uint32_t* ids = nullptr;
+  const void* table = nullptr;
+  int fmt = 0, vocab = 0, D = 0, P = 0, normalize = 0, rec_stride = 16;
+  float* x = nullptr;
+  float* y = nullptr;
+  float* norm = nullptr;
+  const float* gamma = nullptr;
+  float eps = 0.f;
+  _Float16* xn = nullptr;
+  float* rec = nullptr;
+};
+
 struct StagingSlot {
   void* host = nullptr;  // pinned
   size_t cap = 0;
@@ -182,6 +203,7 @@ struct t5h_model {
   std::vector<PendingTiming> pending;
   std::vector<hipEvent_t> event_pool;
   t5h_kernel_stat stats[K_COUNT]{};
+  ReplayRec replay[K_COUNT];
 
   ~t5h_model() {
     if (stream) (void)hipStreamSynchronize(stream);
@@ -495,12 +517,27 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
       a.eps = m->cfg.layer_norm_epsilon;
     }
     HIP_OK(t5k::launch_gemv(epi, W.fmt, a, m->stream));
+    if (m->prof) {
+      ReplayRec& r = m->replay[kind];
+      r.type = ReplayRec::GEMV;
+      r.epi = epi;
+      r.wfmt = W.fmt;
+      r.ga = a;
+    }
     return T5H_OK;
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
   const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
                                             m->gemm_bn_override, m->gemm_tail_override);
   HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
+  if (m->prof) {
+    ReplayRec& r = m->replay[kind];
+    r.type = ReplayRec::GEMM;
+    r.epi = epi;
+    r.wfmt = W.fmt;
+    r.ga = a;
+    r.plan = plan;
+  }
   return T5H_OK;
 }
 
@@ -565,6 +602,20 @@ int validate_cu(const t5h_model* m, const int32_t* cu, int B, int& T) {
   return T5H_OK;
 }
 
+void record_rmsnorm(t5h_model* m, const float* w, int T, float* rec, int stride) {
+  if (!m->prof) return;
+  ReplayRec& r = m->replay[K_RMSNORM];
+  r.type = ReplayRec::RMSNORM;
+  r.x = m->w.x;
+  r.gamma = w;
+  r.xn = m->w.xn;
+  r.n = T;
+  r.D = m->cfg.d_model;
+  r.eps = m->cfg.layer_norm_epsilon;
+  r.rec = rec;
+  r.rec_stride = stride;
+}
+
 // T5LayerNorm of the residual stream into the f16 operand buffer, unless the consuming GEMV
 // fuses it (returns the weight to pass to gemm() then, else nullptr).
 const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
@@ -573,6 +624,7 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
   Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
   const hipError_t e = t5k::launch_rmsnorm(m->w.x, w, m->w.xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon, m->stream);
   if (e != hipSuccess) rc = fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
+  record_rmsnorm(m, w, T, nullptr, 16);
   return nullptr;
 }
 
@@ -582,6 +634,7 @@ int prenorm_rec(t5h_model* m, const float* w, int T) {
   const hipError_t e = t5k::launch_rmsnorm(m->w.x, w, m->w.xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
                                            m->stream, m->w.rec0, rec_stride(m, T));
   if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
+  record_rmsnorm(m, w, T, m->w.rec0, rec_stride(m, T));
   return T5H_OK;
 }
 
@@ -635,6 +688,13 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     a.lutw = m->lutw;
     Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
+    if (m->prof) {
+      ReplayRec& r = m->replay[K_ATTN];
+      r.type = ReplayRec::ATTN;
+      r.aa = a;
+      r.n = nwork;
+      r.D = c.d_kv;
+    }
   }
   if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->w.ao, inner, T, m->w.x, D, 0, nullptr, fold ? &on : nullptr)))
     return rc;
@@ -683,6 +743,22 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
     HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->w.x, m->err_flag, m->stream,
                              g0, c.layer_norm_epsilon, fold ? m->w.xn : nullptr, fold ? m->w.rec0 : nullptr,
                              rec_stride(m, T)));
+    if (m->prof) {
+      ReplayRec& r = m->replay[K_EMBED];
+      r.type = ReplayRec::EMBED;
+      r.ids = d_ids;
+      r.n = T;
+      r.table = m->emb;
+      r.fmt = m->emb_fmt;
+      r.vocab = c.vocab_size;
+      r.D = c.d_model;
+      r.x = m->w.x;
+      r.gamma = g0;
+      r.eps = c.layer_norm_epsilon;
+      r.xn = fold ? m->w.xn : nullptr;
+      r.rec = fold ? m->w.rec0 : nullptr;
+      r.rec_stride = rec_stride(m, T);
+    }
   }
   for (int l = 0; l < c.num_layers; l++) {
     const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : m->final_ln;
@@ -702,6 +778,15 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
   {
     Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
     HIP_OK(t5k::launch_rownorm(d_out, d_norm, T, c.proj_dim, normalize, m->stream));
+    if (m->prof) {
+      ReplayRec& r = m->replay[K_ROWNORM];
+      r.type = ReplayRec::ROWNORM;
+      r.y = d_out;
+      r.norm = d_norm;
+      r.n = T;
+      r.P = c.proj_dim;
+      r.normalize = normalize;
+    }
   }
   return T5H_OK;
 }
@@ -1229,10 +1314,47 @@ int t5h_set_profiling(t5h_model* m, int32_t on) {
   HIP_OK(hipStreamSynchronize(m->stream));
   resolve_timings(m);
   m->prof = on != 0;
+  for (int k = 0; k < K_COUNT; k++) m->replay[k] = ReplayRec{};
   for (int k = 0; k < K_COUNT; k++) {
     m->stats[k].launches = 0;
     m->stats[k].total_ms = m->stats[k].flops = m->stats[k].bytes = 0;
   }
+  return T5H_OK;
+}
+
+int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  if (kind < 0 || kind >= K_COUNT || reps <= 0 || !avg_us) return fail(T5H_ERR_INVALID, "replay: bad arguments");
+  const ReplayRec& r = m->replay[kind];
+  if (r.type == ReplayRec::NONE)
+    return fail(T5H_ERR_INVALID, std::string("replay: no profiled forward launched ") + kKernelNames[kind]);
+  auto launch = [&]() -> hipError_t {
+    switch (r.type) {
+      case ReplayRec::GEMM: return t5k::launch_gemm(r.epi, r.wfmt, r.plan, r.ga, m->stream);
+      case ReplayRec::GEMV: return t5k::launch_gemv(r.epi, r.wfmt, r.ga, m->stream);
+      case ReplayRec::ATTN: return t5k::launch_attention(r.aa, r.n, r.D, m->stream);
+      case ReplayRec::EMBED:
+        return t5k::launch_embed(r.ids, r.n, r.table, r.fmt, r.vocab, r.D, r.x, m->err_flag, m->stream, r.gamma,
+                                 r.eps, r.xn, r.rec, r.rec_stride);
+      case ReplayRec::ROWNORM: return t5k::launch_rownorm(r.y, r.norm, r.n, r.P, r.normalize, m->stream);
+      case ReplayRec::RMSNORM:
+        return t5k::launch_rmsnorm(r.x, r.gamma, r.xn, r.n, r.D, r.eps, m->stream, r.rec, r.rec_stride);
+      default: return hipErrorInvalidValue;
+    }
+  };
+  hipEvent_t e0 = take_event(m), e1 = take_event(m);
+  if (!e0 || !e1) return fail(T5H_ERR_HIP, "replay: event creation failed");
+  HIP_OK(launch());  // warm
+  HIP_OK(hipEventRecord(e0, m->stream));
+  for (int i = 0; i < reps; i++) HIP_OK(launch());
+  HIP_OK(hipEventRecord(e1, m->stream));
+  HIP_OK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+  m->event_pool.push_back(e0);
+  m->event_pool.push_back(e1);
+  *avg_us = (double)ms * 1e3 / reps;
   return T5H_OK;
 }
 

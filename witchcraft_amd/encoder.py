@@ -158,9 +158,16 @@ class T5EncoderModel:
         n = lib.t5h_kernel_stats(self._h, arr, 32)
         if n < 0:
             check(n)
-        return {arr[i].name.decode(): dict(launches=arr[i].launches, total_ms=arr[i].total_ms,
+        return {arr[i].name.decode(): dict(kind=i, launches=arr[i].launches, total_ms=arr[i].total_ms,
                                            flops=arr[i].flops, bytes=arr[i].bytes)
                 for i in range(min(n, 32))}
+
+    def replay_kernel(self, kind: int, reps: int = 20) -> float:
+        """Average microseconds of `reps` back-to-back relaunches of kernel class `kind` (its
+        kernel_stats()[name]["kind"]) from the last profiled forward."""
+        us = C.c_double()
+        check(lib.t5h_replay_kernel(self._h, kind, reps, C.byref(us)))
+        return us.value
 
 
 class T5ModelBuilder:
