@@ -569,3 +569,47 @@ def test_tile_width_does_not_change_bits(enc_mod, xtr):
     finally:
         for h in hs.values():
             h.close()
+
+
+@pytest.mark.parametrize("lens", [[5, 11, 16], [1, 1, 1, 29], [0, 7, 0, 9], [31], [16, 16]])
+def test_small_multi_sequence_batches_vs_oracle(xtr, lens):
+    """Query-sized batches (the small-token GEMV path) holding several sequences, empty ones
+    included: every sequence against the oracle, deterministic across calls."""
+    cfg, _, gpu, ora = xtr
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = np.random.default_rng(400 + int(cu[-1])).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    out, norms = gpu.encode_packed(ids, cu)
+    assert np.isfinite(out).all()
+    assert np.allclose(norms, np.linalg.norm(out, axis=1), rtol=1e-5)
+    for b in range(len(lens)):
+        s, e = int(cu[b]), int(cu[b + 1])
+        if e > s:
+            assert cos_rows(out[s:e], ora.forward(ids[s:e])).min() >= COS_MIN, (lens, b)
+    again, _ = gpu.encode_packed(ids, cu)
+    assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+
+
+def test_two_handles_device_encodes_back_to_back(enc_mod, xtr):
+    """Two handles enqueue device encodes on their own streams without waiting for each other;
+    each result equals the synchronous result bit for bit."""
+    import torch
+    cfg, img, gpu, _ = xtr
+    other = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    try:
+        for T in (32, 300):
+            ids = np.random.default_rng(502 + T).integers(1, cfg["vocab_size"], size=T).astype(np.uint32)
+            cu = np.array([0, T], np.int32)
+            ref, _ = gpu.encode_packed(ids, cu)
+            dev = torch.device("cuda:0")
+            d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+            outs = [torch.empty((T, 128), device=dev) for _ in range(6)]
+            torch.cuda.synchronize()
+            for k in range(6):
+                (gpu if k % 2 == 0 else other).encode_device(d_ids.data_ptr(), cu, outs[k].data_ptr(), None)
+            gpu.synchronize()
+            other.synchronize()
+            for k in range(6):
+                assert np.array_equal(outs[k].cpu().numpy().view(np.uint32), ref.view(np.uint32)), (T, k)
+    finally:
+        other.close()
