@@ -111,6 +111,18 @@ void* t5h_stream(t5h_model* model);
  * Returns T5H_ERR_INVALID if every token is filtered (the reference bails). */
 int t5h_embed_ids(t5h_model* model, const uint32_t* ids, int32_t n_tokens, int32_t max_len,
                   int32_t stride, float* out, int32_t* kept_index, int32_t* n_kept);
+/* Embedder::embed for n_docs documents at once (src/embedder.rs:22-103, called per document
+ * by Gatherer::next, src/lib.rs:930-934).  Document d is ids[doc_offsets[d] .. doc_offsets[d+1])
+ * (doc_offsets[0] = 0, no empty document).  Every window of every document is encoded as one
+ * packed batch; window sums, the norm filter, compaction and normalisation run on the device.
+ * Document d's kept rows are out[kept_offsets[d] .. kept_offsets[d+1]) (out has room for
+ * doc_offsets[n_docs] rows of proj_dim), kept_index[] their positions within the document,
+ * kept_offsets[n_docs + 1].  If a document keeps no token, returns T5H_ERR_INVALID naming it
+ * (the reference's embed bails, :89-91); the outputs of all documents are still written.
+ * Device buffers are grown on demand per handle and reused, not allocated per call. */
+int t5h_embed_batch(t5h_model* model, const uint32_t* ids, const int32_t* doc_offsets, int32_t n_docs,
+                    int32_t max_len, int32_t stride, float* out, int32_t* kept_index,
+                    int32_t* kept_offsets);
 
 /* ---- test hooks (teacher-forced parity checks) ---- */
 

@@ -232,6 +232,96 @@ def test_embedder_windows_vs_oracle(small):
         assert cos_rows(out[gi], ref[ri]).min() >= COS_MIN
 
 
+def _check_embed_docs(gpu, ora, docs, max_len, stride):
+    res = gpu.embed_batch(docs, max_len, stride)
+    assert len(res) == len(docs)
+    for d, (out, kept) in zip(docs, res):
+        ref, kref = ora.embed_ids(d, max_len, stride)
+        assert np.all(np.diff(kept) > 0) and kept.size and kept[-1] < d.size
+        assert np.allclose(np.linalg.norm(out, axis=1), 1.0, atol=1e-5)
+        # tokens near the MIN_NORM threshold may flip; compare the common ones
+        common = np.intersect1d(kept, kref)
+        assert common.size >= 0.95 * max(kept.size, kref.size), (d.size, kept.size, kref.size)
+        gi = np.searchsorted(kept, common)
+        ri = np.searchsorted(kref, common)
+        assert cos_rows(out[gi], ref[ri]).min() >= COS_MIN, d.size
+    return res
+
+
+def test_embed_batch_documents_10_to_5000_tokens_vs_oracle(small):
+    """t5h_embed_batch: windows of every document encoded as one packed batch, summed,
+    filtered and compacted on the device; each document against the oracle's embed_ids."""
+    cfg, _, gpu, ora = small
+    rng = np.random.default_rng(41)
+    lens = [10, 5000, 2047, 2048, 2049, 150, 3841, 1]
+    docs = [rng.integers(1, cfg["vocab_size"], size=n).astype(np.uint32) for n in lens]
+    res = _check_embed_docs(gpu, ora, docs, 2048, 256)
+    # one document per call gives the same rows (windows of one document in its own batch)
+    for d, (out, kept) in zip(docs[:3], res[:3]):
+        o1, k1 = gpu.embed_ids(d, 2048, 256)
+        common = np.intersect1d(kept, k1)
+        assert common.size >= 0.99 * max(kept.size, k1.size)
+        assert cos_rows(out[np.searchsorted(kept, common)], o1[np.searchsorted(k1, common)]).min() >= 0.9999
+    # short windows: many overlaps per token (stride close to max_len) and stride 0
+    _check_embed_docs(gpu, ora, [docs[0], docs[5], docs[6][:700]], 64, 48)
+    _check_embed_docs(gpu, ora, [docs[5], docs[0]], 32, 0)
+
+
+def test_embed_batch_min_norm_filter_vs_oracle(enc_mod):
+    """A projection scaled so that single-window rows straddle MIN_NORM = 1.0 (about half of
+    them dropped) while rows summed over two windows survive: exercises the compaction."""
+    cfg = synth.small_config()
+    img = synth.make_model(cfg, seed=21, std_over={"linear.weight": 0.0055})
+    gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    ora = orc.OracleModel(img, cfg)
+    rng = np.random.default_rng(43)
+    docs = [rng.integers(1, cfg["vocab_size"], size=n).astype(np.uint32) for n in (40, 5000, 2049, 700, 150)]
+    for max_len, stride in [(2048, 256), (64, 48)]:
+        res = _check_embed_docs(gpu, ora, docs, max_len, stride)
+        frac = [k.size / d.size for d, (_, k) in zip(docs, res)]
+        assert min(frac) < 0.9, frac  # the filter dropped tokens
+    # a model whose every row is below the threshold: the reference's embed bails
+    img0 = synth.make_model(cfg, seed=21, std_over={"linear.weight": 0.002})
+    gpu0 = enc_mod.T5EncoderModel.from_gguf(img0, cfg)
+    with pytest.raises(Exception, match="minimum norm"):
+        gpu0.embed_batch(docs[:2], 2048, 256)
+
+
+def test_embed_batch_xtr_windows_vs_oracle(xtr):
+    cfg, _, gpu, ora = xtr
+    rng = np.random.default_rng(42)
+    docs = [rng.integers(1, cfg["vocab_size"], size=n).astype(np.uint32) for n in (10, 1200, 513)]
+    _check_embed_docs(gpu, ora, docs, 512, 128)
+
+
+def test_embed_batch_errors(small):
+    cfg, _, gpu, _ = small
+    ok = np.arange(1, 40, dtype=np.uint32)
+    for docs, ml, st in [([ok, ok[:0]], 2048, 256),           # empty document
+                         ([ok], 64, 64), ([ok], 0, 0),         # stride >= max_len, max_len 0
+                         ([ok], 1 << 20, 256),                 # window longer than max_seq_len
+                         ([ok, np.array([cfg["vocab_size"]], np.uint32)], 2048, 256)]:
+        with pytest.raises(Exception):
+            gpu.embed_batch(docs, ml, st)
+    assert len(gpu.embed_batch([ok], 2048, 256)) == 1  # the handle still works
+
+
+def test_workspace_growth_orders_clear_before_uploads(enc_mod, small):
+    """Each call grows a fresh handle's workspace (more tokens, then more sequences); the
+    cleared buffers must be in place before the call's own uploads land on the handle's stream."""
+    cfg, img, _, ora = small
+    gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    rng = np.random.default_rng(44)
+    for lens in ([16], [2048] * 8, [64] * 300, [2048] * 16):
+        cu = np.zeros(len(lens) + 1, np.int32)
+        cu[1:] = np.cumsum(lens)
+        ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+        out, _ = gpu.encode_packed(ids, cu)
+        for b in (0, len(lens) - 1):
+            ref = ora.forward(ids[cu[b]:cu[b + 1]])
+            assert cos_rows(out[cu[b]:cu[b + 1]], ref).min() >= COS_MIN, (lens[0], len(lens), b)
+
+
 def test_hybrid_layout_f32_attention_weights(enc_mod):
     """cfg5 layout: F32 q/k/v/o/wo (kept as f16 on the device), Q4_K wi_0/wi_1/linear."""
     cfg = synth.small_config()

@@ -172,6 +172,11 @@ struct WorkChunk {
   int start[CAP], len[CAP], wofs[CAP];
 };
 hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s);
-hipError_t launch_window_sum(const float* win_out, const int* src_rows, int n_tokens, int max_windows,
-                             int P, float* sum, float* norm, float* normalized, hipStream_t s);
+// Embedder post-processing over a batch of documents (k_embed.hip): win = packed window outputs,
+// docs[d] = (first token, tokens, first window row, windows), tok_doc[t] = document of token t.
+hipError_t launch_embed_batch(const float* win, const int4* docs, const int* tok_doc, int N, int max_len, int stride,
+                              int P, float* norms, uint8_t* flags, int* block_counts, int* block_offsets, float* out,
+                              int* kept_index, int* kept_offsets, hipStream_t s);
+// Blocks of tokens the embed kernels use for N tokens (block_counts / block_offsets need one more).
+int embed_batch_blocks(int N);
 }  // namespace t5k

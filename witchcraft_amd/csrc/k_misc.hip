@@ -1,5 +1,5 @@
 // k_misc.hip -- memory-bound kernels around the GEMMs: embedding gather, T5 RMSNorm,
-// row norms / L2 normalisation, window summation of the embedder.
+// row norms / L2 normalisation.
 #include "common.hpp"
 
 namespace {
@@ -252,33 +252,6 @@ __global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restr
   if (i < n) y[tiled_index(i / K, i % K, K)] = (_Float16)x[i];
 }
 
-// Embedder window summation (src/embedder.rs:38-63): token t's row is the sum, in window
-// order, of the rows src_rows[t*max_windows + w] (>= 0) of the per-window outputs.  Also
-// emits the pre-normalisation norm (:83) and the normalised row (:94).
-__global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict__ win,
-                                                         const int* __restrict__ src, int n, int maxw,
-                                                         int P, float* __restrict__ sum,
-                                                         float* __restrict__ norm,
-                                                         float* __restrict__ normalized) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= n) return;
-  const int lane = threadIdx.x & 63;
-  float ss = 0.f;
-  for (int i = lane; i < P; i += 64) {
-    float a = 0.f;
-    for (int w = 0; w < maxw; w++) {
-      const int r = src[t * maxw + w];
-      if (r >= 0) a += win[(size_t)r * P + i];
-    }
-    sum[(size_t)t * P + i] = a;
-    ss += a * a;
-  }
-  ss = wave_sum(ss);
-  const float nv = sqrtf(ss);
-  if (lane == 0) norm[t] = nv;
-  for (int i = lane; i < P; i += 64) normalized[(size_t)t * P + i] = sum[(size_t)t * P + i] / nv;
-}
-
 // Attention work list from by-value arguments (no host staging buffer): item wofs[i] + q of
 // sequence i is (start[i], len[i], 64 q, 0), the layout upload_batch writes.
 __global__ __launch_bounds__(256) void work_list_kernel(t5k::WorkChunk c, int4* __restrict__ work) {
@@ -322,13 +295,6 @@ hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s) {
   if (c.n <= 0) return hipSuccess;
   if (c.n > WorkChunk::CAP) return hipErrorInvalidValue;
   hipLaunchKernelGGL(work_list_kernel, dim3((c.n + 255) / 256), dim3(256), 0, s, c, work);
-  return hipGetLastError();
-}
-hipError_t launch_window_sum(const float* win, const int* src, int n, int maxw, int P, float* sum,
-                             float* norm, float* normalized, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(window_sum_kernel, dim3((n + 3) / 4), dim3(256), 0, s, win, src, n, maxw, P, sum,
-                     norm, normalized);
   return hipGetLastError();
 }
 }  // namespace t5k

@@ -35,7 +35,6 @@ struct PkWin {
   long long hdr, data;    // scratch offsets (encode) / input offsets of perm+pairs, stream (decode)
   int m, dlen, err, pad;  // filled by pk_quant / pk_rans_enc; decode: m and dlen are inputs
 };
-constexpr int PK_HDR_BYTES = 256 + 2 + 4 * 4096 + 254;  // per-window slot: perm bytes, u16 m, pairs
 }  // namespace t5k
 
 namespace {

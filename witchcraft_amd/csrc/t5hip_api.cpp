@@ -192,6 +192,10 @@ struct t5h_model {
   unsigned* err_flag = nullptr;
   void* scratch = nullptr;  // this device's address of the no-alloc scratch array
 
+  // ---- embedder post-processing (t5h_embed_batch), grown on demand ----
+  void* ew = nullptr;
+  size_t ew_bytes = 0;
+
   // ---- host staging ----
   StagingSlot slots[4];
   int next_slot = 0;
@@ -219,6 +223,7 @@ struct t5h_model {
     }
     for (auto e : event_pool) (void)hipEventDestroy(e);
     if (ws) (void)hipFree(ws);
+    if (ew) (void)hipFree(ew);
     if (arena) (void)hipFree(arena);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -380,7 +385,9 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
     m->cap_tokens = m->cap_seqs = m->cap_work = 0;
     return fail(T5H_ERR_NOMEM, "workspace allocation of " + std::to_string(off) + " bytes failed");
   }
-  HIP_OK(hipMemset(m->ws, 0, off));
+  // On the handle's own stream: hipMemset runs on the null stream, which a non-blocking stream
+  // does not wait for, so the clear could land after the uploads that follow on m->stream.
+  HIP_OK(hipMemsetAsync(m->ws, 0, off, m->stream));
   m->ws_bytes = off;
   carve_workspace(m, tpad, capW, (uint8_t*)m->ws, m->w);
   m->cap_tokens = tpad - 128;
@@ -890,6 +897,103 @@ int encode_host(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B,
   return T5H_OK;
 }
 
+// Embedder::embed for a batch of documents (src/embedder.rs:22-103, once per document from
+// src/lib.rs:930-934): every window of every document encoded as one packed batch, then the
+// window sums, MIN_NORM filter, compaction and L2 normalisation on the device (k_embed.hip).
+// Host buffers; out / kept_index have room for every token, kept_offsets[n_docs + 1].
+int embed_batch_impl(t5h_model* m, const uint32_t* ids, const int32_t* doc_off, int n_docs, int max_len, int stride,
+                     float* out, int32_t* kept_index, int32_t* kept_offsets) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  if (!ids || !doc_off || !out || !kept_index || !kept_offsets || n_docs <= 0)
+    return fail(T5H_ERR_INVALID, "embed: bad arguments");
+  if (max_len <= 0 || max_len > m->cfg.max_seq_len || stride < 0 || stride >= max_len)
+    return fail(T5H_ERR_INVALID, "embed: need 0 < max_len <= max_seq_len and 0 <= stride < max_len");
+  if (doc_off[0] != 0) return fail(T5H_ERR_INVALID, "embed: doc_offsets[0] must be 0");
+  for (int d = 0; d < n_docs; d++)
+    if (doc_off[d + 1] <= doc_off[d])
+      return fail(T5H_ERR_INVALID, "embed: document " + std::to_string(d) + " is empty");
+  const int N = doc_off[n_docs], P = m->cfg.proj_dim, step = max_len - stride;
+  for (int t = 0; t < N; t++)
+    if (ids[t] >= (uint32_t)m->cfg.vocab_size)
+      return fail(T5H_ERR_INVALID, "token id " + std::to_string(ids[t]) + " at position " + std::to_string(t) +
+                                       " outside the vocabulary");
+  // Windows of src/embedder.rs:38-63: start_k = k * (max_len - stride) until a window reaches the
+  // end; every window but a document's last holds max_len tokens.
+  std::vector<int32_t> cu{0};
+  std::vector<int4> docs(n_docs);
+  for (int d = 0; d < n_docs; d++) {
+    const int n = doc_off[d + 1] - doc_off[d];
+    const int nwin = n <= max_len ? 1 : (n - max_len + step - 1) / step + 1;
+    docs[d] = make_int4(doc_off[d], n, cu.back(), nwin);
+    for (int k = 0; k < nwin; k++) cu.push_back(cu.back() + std::min(max_len, n - k * step));
+  }
+  const int W = n_docs ? (int)cu.size() - 1 : 0, T = cu.back();
+  if ((rc = ensure_workspace(m, T, W, (T + 63) / 64 + W))) return rc;
+  // device buffers of the post-processing
+  const int nb = t5k::embed_batch_blocks(N);
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off = align256(off + n);
+    return o;
+  };
+  const size_t o_doc = take((size_t)n_docs * sizeof(int4)), o_tdoc = take((size_t)N * 4), o_nrm = take((size_t)N * 4),
+               o_flag = take(N), o_cnt = take((size_t)(nb + 1) * 4), o_boff = take((size_t)(nb + 1) * 4),
+               o_out = take((size_t)N * P * 4), o_kidx = take((size_t)N * 4), o_koff = take((size_t)(n_docs + 1) * 4);
+  if (off > m->ew_bytes) {
+    if (m->ew) {
+      HIP_OK(hipStreamSynchronize(m->stream));
+      HIP_OK(hipFree(m->ew));
+      m->ew = nullptr;
+      m->ew_bytes = 0;
+    }
+    if (hipMalloc(&m->ew, off) != hipSuccess) return fail(T5H_ERR_NOMEM, "embed workspace allocation failed");
+    m->ew_bytes = off;
+  }
+  uint8_t* e = (uint8_t*)m->ew;
+  // uploads through the pinned staging buffer: window ids, documents, token -> document
+  const size_t h_ids = 0, h_doc = align256((size_t)T * 4), h_tdoc = h_doc + align256((size_t)n_docs * sizeof(int4));
+  const size_t h_end = h_tdoc + align256((size_t)N * 4);
+  const size_t h_dl = align256((size_t)(n_docs + 1) * 4) + (size_t)N * 4 + (size_t)N * P * 4;  // downloads
+  if ((rc = ensure_io(m, std::max(h_end, h_dl)))) return rc;
+  uint8_t* io = (uint8_t*)m->io;
+  {
+    uint32_t* wid = (uint32_t*)(io + h_ids);
+    int* tdoc = (int*)(io + h_tdoc);
+    for (int d = 0, w = 0; d < n_docs; d++) {
+      for (int k = 0; k < docs[d].w; k++, w++)
+        memcpy(wid + cu[w], ids + doc_off[d] + k * step, (size_t)(cu[w + 1] - cu[w]) * 4);
+      for (int t = doc_off[d]; t < doc_off[d + 1]; t++) tdoc[t] = d;
+    }
+    memcpy(io + h_doc, docs.data(), (size_t)n_docs * sizeof(int4));
+  }
+  HIP_OK(hipMemcpyAsync(m->w.ids, io + h_ids, (size_t)T * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_OK(hipMemcpyAsync(e + o_doc, io + h_doc, (size_t)n_docs * sizeof(int4), hipMemcpyHostToDevice, m->stream));
+  HIP_OK(hipMemcpyAsync(e + o_tdoc, io + h_tdoc, (size_t)N * 4, hipMemcpyHostToDevice, m->stream));
+  if ((rc = enqueue_forward(m, m->w.ids, cu.data(), W, T, m->w.out, nullptr, 0))) return rc;
+  HIP_OK(t5k::launch_embed_batch(m->w.out, (const int4*)(e + o_doc), (const int*)(e + o_tdoc), N, max_len, stride, P,
+                                 (float*)(e + o_nrm), e + o_flag, (int*)(e + o_cnt), (int*)(e + o_boff),
+                                 (float*)(e + o_out), (int*)(e + o_kidx), (int*)(e + o_koff), m->stream));
+  // first the offsets and the total, then exactly the kept rows
+  int32_t* h_koff = (int32_t*)io;
+  HIP_OK(hipMemcpyAsync(h_koff, e + o_koff, (size_t)n_docs * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(h_koff + n_docs, e + o_boff + (size_t)nb * 4, 4, hipMemcpyDeviceToHost, m->stream));
+  if ((rc = finish_sync(m))) return rc;
+  const int total = h_koff[n_docs];
+  memcpy(kept_offsets, h_koff, (size_t)(n_docs + 1) * 4);
+  uint8_t* dl = io + align256((size_t)(n_docs + 1) * 4);
+  HIP_OK(hipMemcpyAsync(dl, e + o_out, (size_t)total * P * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipMemcpyAsync(dl + (size_t)total * P * 4, e + o_kidx, (size_t)total * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_OK(hipStreamSynchronize(m->stream));
+  memcpy(out, dl, (size_t)total * P * 4);
+  memcpy(kept_index, dl + (size_t)total * P * 4, (size_t)total * 4);
+  for (int d = 0; d < n_docs; d++)
+    if (kept_offsets[d + 1] == kept_offsets[d])  // Embedder::embed bails for such a document (:89-91)
+      return fail(T5H_ERR_INVALID, "document " + std::to_string(d) + ": all token embeddings below minimum norm threshold");
+  return T5H_OK;
+}
+
 int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_device, t5h_model** out) {
   if (!out) return fail(T5H_ERR_INVALID, "out is NULL");
   *out = nullptr;
@@ -1151,66 +1255,17 @@ void* t5h_stream(t5h_model* m) { return m ? (void*)m->stream : nullptr; }
 
 int t5h_embed_ids(t5h_model* m, const uint32_t* ids, int32_t n, int32_t max_len, int32_t stride,
                   float* out, int32_t* kept_index, int32_t* n_kept) {
-  int rc;
-  if ((rc = check_model(m))) return rc;
-  if (!ids || !out || !kept_index || !n_kept || n <= 0)
-    return fail(T5H_ERR_INVALID, "embed_ids: bad arguments");
-  if (max_len <= 0 || max_len > m->cfg.max_seq_len || stride < 0 || stride >= max_len)
-    return fail(T5H_ERR_INVALID, "embed_ids: need 0 < max_len <= max_seq_len and 0 <= stride < max_len");
-  // Windows of src/embedder.rs:38-63.
-  std::vector<int> wstart, wend;
-  for (int start = 0;;) {
-    const int end = std::min(start + max_len, n);
-    wstart.push_back(start);
-    wend.push_back(end);
-    if (end == n) break;
-    start = end > stride ? end - stride : 0;
-  }
-  const int W = (int)wstart.size();
-  std::vector<int32_t> cu(W + 1, 0);
-  std::vector<uint32_t> wids;
-  for (int w = 0; w < W; w++) {
-    cu[w + 1] = cu[w] + (wend[w] - wstart[w]);
-    wids.insert(wids.end(), ids + wstart[w], ids + wend[w]);
-  }
-  std::vector<int> cover(n, 0);
-  int maxw = 1;
-  for (int w = 0; w < W; w++)
-    for (int t = wstart[w]; t < wend[w]; t++) maxw = std::max(maxw, ++cover[t]);
-  std::vector<int> src((size_t)n * maxw, -1);
-  std::fill(cover.begin(), cover.end(), 0);
-  for (int w = 0; w < W; w++)
-    for (int t = wstart[w]; t < wend[w]; t++) src[(size_t)t * maxw + cover[t]++] = cu[w] + (t - wstart[w]);
-  const int P = m->cfg.proj_dim, T = cu[W];
-  std::vector<float> win((size_t)T * P);
-  if ((rc = encode_host(m, wids.data(), cu.data(), W, win.data(), nullptr, 0))) return rc;
-  // Window sum + norms + normalisation on the device.
-  float* d_buf = nullptr;
-  const size_t need = (size_t)T * P * 4 + (size_t)n * maxw * 4 + (size_t)n * P * 8 + (size_t)n * 4 + 1024;
-  HIP_OK(hipMalloc(&d_buf, need));
-  std::unique_ptr<void, void (*)(void*)> guard(d_buf, [](void* p) { (void)hipFree(p); });
-  float* d_win = d_buf;
-  int* d_src = (int*)(d_win + (size_t)T * P);
-  float* d_sum = (float*)(d_src + (size_t)n * maxw);
-  float* d_nrm = d_sum + (size_t)n * P;
-  float* d_nz = d_nrm + n;
-  HIP_OK(hipMemcpyAsync(d_win, win.data(), (size_t)T * P * 4, hipMemcpyHostToDevice, m->stream));
-  HIP_OK(hipMemcpyAsync(d_src, src.data(), src.size() * 4, hipMemcpyHostToDevice, m->stream));
-  HIP_OK(t5k::launch_window_sum(d_win, d_src, n, maxw, P, d_sum, d_nrm, d_nz, m->stream));
-  std::vector<float> nz((size_t)n * P), nrm(n);
-  HIP_OK(hipMemcpyAsync(nz.data(), d_nz, nz.size() * 4, hipMemcpyDeviceToHost, m->stream));
-  HIP_OK(hipMemcpyAsync(nrm.data(), d_nrm, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
-  HIP_OK(hipStreamSynchronize(m->stream));
-  int k = 0;
-  for (int t = 0; t < n; t++) {
-    if (nrm[t] >= 1.0f) {  // MIN_NORM, src/embedder.rs:79-88
-      memcpy(out + (size_t)k * P, nz.data() + (size_t)t * P, (size_t)P * 4);
-      kept_index[k++] = t;
-    }
-  }
-  *n_kept = k;
-  if (k == 0) return fail(T5H_ERR_INVALID, "all token embeddings below minimum norm threshold");
-  return T5H_OK;
+  if (!n_kept || n <= 0) return fail(T5H_ERR_INVALID, "embed_ids: bad arguments");
+  const int32_t doc[2] = {0, n};
+  int32_t kept_off[2] = {0, 0};
+  const int rc = embed_batch_impl(m, ids, doc, 1, max_len, stride, out, kept_index, kept_off);
+  *n_kept = kept_off[1];
+  return rc;
+}
+
+int t5h_embed_batch(t5h_model* m, const uint32_t* ids, const int32_t* doc_offsets, int32_t n_docs, int32_t max_len,
+                    int32_t stride, float* out, int32_t* kept_index, int32_t* kept_offsets) {
+  return embed_batch_impl(m, ids, doc_offsets, n_docs, max_len, stride, out, kept_index, kept_offsets);
 }
 
 int t5h_q4k_dequant_f32(const void* blocks, size_t nblk, float* out, int hip_device) {

@@ -135,6 +135,19 @@ class T5EncoderModel:
         check(lib.t5h_embed_ids(self._h, ids, ids.size, max_len, stride, out, kept, C.byref(nk)))
         return out[: nk.value], kept[: nk.value]
 
+    def embed_batch(self, docs, max_len: int = 2048, stride: int = 256):
+        """Embedder::embed on several token-id documents in one packed encode
+        (src/embedder.rs:22-103 per document) -> [(rows [n_kept, proj], kept positions)]."""
+        docs = [np.ascontiguousarray(d, np.uint32).reshape(-1) for d in docs]
+        offs = np.zeros(len(docs) + 1, np.int32)
+        offs[1:] = np.cumsum([d.size for d in docs])
+        ids = np.concatenate(docs) if docs else np.zeros(0, np.uint32)
+        out = np.empty((ids.size, self.cfg.proj_dim), np.float32)
+        kept = np.empty(ids.size, np.int32)
+        koff = np.zeros(len(docs) + 1, np.int32)
+        check(lib.t5h_embed_batch(self._h, ids, offs, len(docs), max_len, stride, out, kept, koff))
+        return [(out[koff[d]:koff[d + 1]], kept[koff[d]:koff[d + 1]]) for d in range(len(docs))]
+
     # ---- test hooks ----
     def layer_forward(self, layer: int, x: np.ndarray, cu_seqlens: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)
