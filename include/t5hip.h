@@ -124,6 +124,14 @@ int t5h_embed_batch(t5h_model* model, const uint32_t* ids, const int32_t* doc_of
                     int32_t max_len, int32_t stride, float* out, int32_t* kept_index,
                     int32_t* kept_offsets);
 
+/* ---- offline weight quantization (host only, no device needed) ---- */
+
+/* f32 values -> GGML Q4_K super-blocks (144 bytes per 256 values): the quantize tool's
+ * QTensor::quantize(_, Q4K) (tools/quantize-tool/src/main.rs:12-24), i.e. candle's
+ * BlockQ4K::from_float with GGML's make_qkx1_quants scale/min search.  n_values % 256 == 0;
+ * out receives n_values / 256 * 144 bytes.  threads <= 0: up to 16 host threads. */
+int t5h_quantize_q4k(const float* x, int64_t n_values, uint8_t* out, int32_t threads);
+
 /* ---- test hooks (teacher-forced parity checks) ---- */
 
 /* Q4_K -> f32, bit-exact with candle BlockQ4K::to_float (reached from

@@ -347,9 +347,10 @@ def test_xtr_hybrid_layout_large_batch_vs_oracle(enc_mod):
         gpu.close()
 
 
-def test_q4k_embedding_table(enc_mod):
+@pytest.mark.parametrize("emb_format", ["q4k", "f32"])
+def test_embedding_table_formats(enc_mod, emb_format):
     cfg = synth.small_config()
-    img = synth.make_model(cfg, seed=41, emb_format="q4k")
+    img = synth.make_model(cfg, seed=41, emb_format=emb_format)
     gpu = enc_mod.T5EncoderModel.from_gguf(img, cfg)
     ora = orc.OracleModel(img, cfg)
     ids, cu = synth.ragged_batch(2, 10, 80, cfg["vocab_size"], seed=13)

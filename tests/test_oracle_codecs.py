@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from witchcraft_amd.quantize import quantize_q4k
+from witchcraft_amd.quantize import quantize_q4k, quantize_q4k_minmax
 
 GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
 
@@ -91,7 +91,7 @@ def test_q4k_special_cases():
 def test_quantizer_roundtrip_and_format():
     rng = np.random.default_rng(0)
     x = (rng.standard_normal((32, 768)) * 0.02).astype(np.float32)
-    q = quantize_q4k(x)
+    q = quantize_q4k_minmax(x)
     assert q.shape == (32, 3 * 144)
     y = orc.q4k_dequant(q).reshape(32, 768)
     rel = np.linalg.norm(y - x) / np.linalg.norm(x)
@@ -101,7 +101,7 @@ def test_quantizer_roundtrip_and_format():
     step = (np.maximum(xb.max(1), 0) - np.minimum(xb.min(1), 0)) / 15
     assert np.all(np.abs(xb - yb).max(1) <= 1.6 * step + 1e-6)
     # zero rows quantize to exact zeros
-    z = orc.q4k_dequant(quantize_q4k(np.zeros((2, 256), np.float32)))
+    z = orc.q4k_dequant(quantize_q4k_minmax(np.zeros((2, 256), np.float32)))
     assert np.all(z == 0)
 
 

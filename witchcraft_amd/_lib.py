@@ -56,6 +56,7 @@ SIGNATURES = {
     "t5h_embed_ids": (C.c_int, [_vp, _u32p, C.c_int32, C.c_int32, C.c_int32, _f32p, _i32p,
                                 C.POINTER(C.c_int32)]),
     "t5h_embed_batch": (C.c_int, [_vp, _u32p, _i32p, C.c_int32, C.c_int32, C.c_int32, _f32p, _i32p, _i32p]),
+    "t5h_quantize_q4k": (C.c_int, [_f32p, C.c_int64, _u8p, C.c_int32]),
     "t5h_q4k_dequant_f32": (C.c_int, [_u8p, C.c_size_t, _f32p, C.c_int]),
     "t5h_matmul_t": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _f32p]),
     "t5h_matmul_argmax": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _u32p]),
