@@ -358,16 +358,26 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
         LOAD_A((u + S - 1) % S, min(kt + S - 1, nkt - 1));
         __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's MFMAs
         const _Float16* bsrc = bbase + (kt & 1) * (BN * LDSK);
+        // Weight fragments j = s * NB + nb in order, each read FD fragments ahead of its MFMAs
+        // so that the LDS latency hides behind the MFMAs of the fragments before it; the
+        // scheduling barriers keep the compiler from regrouping the reads.
+        constexpr int NF = 2 * NB, FD = 2;
+        h8 wf[FD + 1];
 #pragma unroll
-        for (int s = 0; s < 2; s++)
+        for (int j = 0; j < FD; j++)
+          wf[j] = *reinterpret_cast<const h8*>(bsrc + (j % NB) * 16 * LDSK + 32 * (j / NB));
 #pragma unroll
-          for (int nb = 0; nb < NB; nb++) {  // one weight fragment live at a time
-            const h8 wf = *reinterpret_cast<const h8*>(bsrc + nb * 16 * LDSK + 32 * s);
+        for (int j = 0; j < NF; j++) {
+          if (j + FD < NF)
+            wf[(j + FD) % (FD + 1)] =
+                *reinterpret_cast<const h8*>(bsrc + ((j + FD) % NB) * 16 * LDSK + 32 * ((j + FD) / NB));
+          const int s = j / NB, nb = j % NB;
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-              acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, __builtin_bit_cast(h8, a[u][mb][s]),
-                                                                    acc[mb][nb], 0, 0, 0);
-          }
+          for (int mb = 0; mb < MB; mb++)
+            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j % (FD + 1)], __builtin_bit_cast(h8, a[u][mb][s]),
+                                                                  acc[mb][nb], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         __syncthreads();
       }
     }
