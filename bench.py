@@ -612,7 +612,7 @@ def main() -> None:
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": f"{args.workload}: {desc}", "global_batch": n_seqs, "seq_len": pad,
-                   "tokens_per_step": T, "weights": "random-init N(0,0.02^2), Q4_K (own quantizer)",
+                   "tokens_per_step": T, "weights": "random-init N(0,0.02^2), Q4_K by the quantize tool's scale/min search (t5h_quantize_q4k); f32 embeddings and norms",
                    "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": base, "kernels": kernels,
     }

@@ -745,7 +745,11 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
   // With folded norms the embedding gather also emits the first norm's operand and records.
   const bool fold = fold_norm(m, T);
   {
-    Timed t(m, K_EMBED, 0, (double)T * c.d_model * 8);
+    // algorithmic bytes: the table rows read (f32, or 144 B per 256 values of a Q4_K table), x
+    // written (f32), and with the folded norm the f16 operand and the 64-byte record per token
+    const double row_in = m->emb_fmt == EMB_F32 ? c.d_model * 4.0 : c.d_model / 256.0 * 144.0;
+    const double row_out = c.d_model * 4.0 + (fold ? c.d_model * 2.0 + 64.0 : 0.0);
+    Timed t(m, K_EMBED, 0, (double)T * (row_in + row_out));
     const float* g0 = c.num_layers > 0 ? m->layers[0].ln0 : m->final_ln;
     HIP_OK(t5k::launch_embed(d_ids, T, m->emb, m->emb_fmt, c.vocab_size, c.d_model, m->w.x, m->err_flag, m->stream,
                              g0, c.layer_norm_epsilon, fold ? m->w.xn : nullptr, fold ? m->w.rec0 : nullptr,

@@ -5,7 +5,7 @@ The reference loads `assets/xtr.gguf` converted from google/xtr-base-en
 offline, so tests and benchmarks build random-init models of the same architecture
 and tensor names (src/quantized_t5.rs:216-221,323-355,514-516,582-590,640-690):
 
-  encoder.embed_tokens.weight                             [vocab, d_model]  Q4_K N(0,1)
+  encoder.embed_tokens.weight                             [vocab, d_model]  F32 N(0,1)
   encoder.block.{i}.layer.0.SelfAttention.{q,k,v}.weight  [inner, d_model]  Q4_K N(0,0.02^2)
   encoder.block.{i}.layer.0.SelfAttention.o.weight        [d_model, inner]  Q4_K
   encoder.block.0.layer.0.SelfAttention.relative_attention_bias.weight [buckets, heads] F32
@@ -15,11 +15,12 @@ and tensor names (src/quantized_t5.rs:216-221,323-355,514-516,582-590,640-690):
   encoder.final_layer_norm.weight                         [d_model]         F32
   linear.weight                                           [128, d_model]    Q4_K
 
-Q4_K tensors are quantized by `quantize.quantize_q4k`, the quantize tool's scale/min search;
-as in that tool (tools/quantize-tool/src/main.rs:17-22) every rank-2 tensor whose second
-dimension is a multiple of 256 is Q4_K, the embedding table included (`emb_format="f32"`
-keeps it F32).  `layout="hybrid"` stores q/k/v/o/wo as F32 (the `hybrid-dequant` feature's
-dense weights) and keeps wi_0/wi_1/linear Q4_K.  Every tensor draws from its own generator
+Q4_K tensors are quantized by `quantize.quantize_q4k`, the quantize tool's scale/min search.
+The benchmark configurations keep the embedding table F32; `emb_format="q4k"` gives the
+quantize tool's own layout (tools/quantize-tool/src/main.rs:17-22: every rank-2 tensor whose
+second dimension is a multiple of 256 is Q4_K, the embedding table included).
+`layout="hybrid"` stores q/k/v/o/wo as F32 (the `hybrid-dequant` feature's dense weights)
+and keeps wi_0/wi_1/linear Q4_K.  Every tensor draws from its own generator
 seeded by (seed, crc32(name)), so any subset is reproducible on any host.
 """
 from __future__ import annotations
@@ -71,7 +72,7 @@ def _normal(seed: int, name: str, shape, std: float) -> np.ndarray:
     return (_rng(seed, name).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
 
-def make_model(cfg: dict = XTR_BASE, seed: int = 0, layout: str = "q4k", emb_format: str = "q4k",
+def make_model(cfg: dict = XTR_BASE, seed: int = 0, layout: str = "q4k", emb_format: str = "f32",
                norm_jitter: float = 0.1, bias_std: float | None = None,
                std_over: dict | None = None) -> bytes:
     """Build a GGUF image of a random-init encoder.
