@@ -132,6 +132,25 @@ def test_matmul_t_q4_matches_decode_then_matmul(codec):
     assert np.all(np.abs(fused.astype(np.float64) - two_step) <= bound)
 
 
+def test_matmul_t_q4_query_beyond_bf16_range(codec):
+    """Finite query values of magnitude >= 0x7f7f8000 (about 3.396e38) round to a bf16 infinity,
+    so the three-way bf16 split cannot carry them: their block takes the f32 kernel and gives
+    the finite f32 scores.  A value just below the threshold stays on the split path."""
+    from witchcraft_amd import score
+    rng = np.random.default_rng(32)
+    codes = rng.integers(0, 256, (4096, 64)).astype(np.uint8)  # the streaming shape: M <= 32
+    r = orc.residual_decode(codes, 128).astype(np.float64)
+    for big in (np.float32(3.4e38), -np.float32(3.39e38)):
+        a = _unit_rows(20, 128, rng)
+        a[2, 5] = big
+        got = codec.matmul_t_q4(a, codes)
+        two_step = score.matmul_t(a, codec.from_companded_q4_bytes(codes, 128))
+        assert np.all(np.isfinite(two_step)) and np.all(np.isfinite(got)), big
+        want = a.astype(np.float64) @ r.T
+        bound = 3 * 128 * 2.0 ** -23 * (np.abs(a).astype(np.float64) @ np.abs(r).T)
+        assert np.all(np.abs(got - want) <= bound), big
+
+
 def test_matmul_t_q4_shape_errors(codec):
     with pytest.raises(ValueError):
         codec.matmul_t_q4(np.zeros((2, 128), np.float32), np.zeros((3, 32), np.uint8))

@@ -322,6 +322,48 @@ def test_workspace_growth_orders_clear_before_uploads(enc_mod, small):
             assert cos_rows(out[cu[b]:cu[b + 1]], ref).min() >= COS_MIN, (lens[0], len(lens), b)
 
 
+def test_large_norm_weights_vs_oracle(enc_mod):
+    """T5LayerNorm weights with 30x the default spread (|gamma| up to ~12): the f16 operands
+    (folded: x * gamma * s with s about 1/16 of the previous inverse RMS; unfolded:
+    x * inv * gamma) and the gated FFN intermediate stay inside the f16 range, and the
+    embeddings match the oracle on both paths.  (Much larger weights make the unscaled T5
+    attention scores so large that f16 operand rounding alone moves the softmax: 100x the
+    spread gives cosines near 0.98 with finite values.)"""
+    cfg = synth.small_config()
+    img = synth.make_model(cfg, seed=51, norm_jitter=3.0)
+    ora = orc.OracleModel(img, cfg)
+    ids, cu = synth.ragged_batch(4, 20, 150, cfg["vocab_size"], seed=52)
+    for fold in ("1", "0"):
+        h = _handle_with_env(enc_mod, img, cfg, T5H_FOLD_NORM=fold)
+        try:
+            _check_batch(h, ora, ids, cu)
+        finally:
+            h.close()
+
+
+def test_f16_operand_overflow_is_reported(enc_mod, small):
+    """A norm weight so large that x * gamma leaves the f16 range turns the embeddings into
+    inf / NaN; the row-norm kernel flags it and the call fails instead of returning them."""
+    from witchcraft_amd import gguf
+    from witchcraft_amd._lib import T5HError
+    cfg, img, gpu, ora = small
+    ts = gguf.read_gguf(img)
+    name = "encoder.final_layer_norm.weight"
+    w = np.frombuffer(ts[name].data, np.float32).copy()
+    w[3] = 3e9
+    ts[name] = gguf.Tensor(name, ts[name].ggml_type, ts[name].shape, w.tobytes())
+    bad = enc_mod.T5EncoderModel.from_gguf(gguf.write_gguf(list(ts.values())), cfg)
+    ids, cu = synth.ragged_batch(3, 10, 60, cfg["vocab_size"], seed=53)
+    try:
+        for _ in range(2):  # the flag is cleared after each report
+            with pytest.raises(T5HError, match="non-finite"):
+                bad.encode_packed(ids, cu)
+        # the other handle is unaffected
+        _check_batch(gpu, ora, ids, cu)
+    finally:
+        bad.close()
+
+
 def test_hybrid_layout_f32_attention_weights(enc_mod):
     """cfg5 layout: F32 q/k/v/o/wo (kept as f16 on the device), Q4_K wi_0/wi_1/linear."""
     cfg = synth.small_config()

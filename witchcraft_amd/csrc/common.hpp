@@ -158,7 +158,9 @@ hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, 
 // rec: when set, record mode for a consuming GEMM that folds the norm (GemmArgs::rec).
 hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, int D, float eps,
                           hipStream_t s, float* rec = nullptr, int rec_stride = 16);
-hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s);
+// err (may be null): set to 1 when a row's norm is not finite.
+hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s,
+                          unsigned* err = nullptr);
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s);
 // Query-side scoring: C = A . B^T (f32) and its per-row argmax (k_score.hip).
 hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int N, int D, bool bf16_b,

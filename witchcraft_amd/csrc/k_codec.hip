@@ -261,10 +261,12 @@ __global__ __launch_bounds__(256, 2) void matmul_t_q4_split_kernel(const float* 
     split3(tab.v[x >> 4], h0, m0, l0);
     split3(tab.v[x & 15], h1, m1, l1);
     pt[x] = make_uint4(h0 | (h1 << 16), m0 | (m1 << 16), l0 | (l1 << 16), 0u);
+    // Non-finite values, and finite ones of magnitude >= 0x7f7f8000 (which round to a bf16
+    // infinity in split3, so x - inf would give NaN), take the f32 kernel.
     int nf = 0;
     for (int e = threadIdx.x; e < 16 * MB * D; e += 256) {
       const int r = e / D;
-      if (r < M && !__builtin_isfinite(A[(size_t)r * D + (e - r * D)])) nf = 1;
+      if (r < M && !(fabsf(A[(size_t)r * D + (e - r * D)]) < __uint_as_float(0x7f7f8000u))) nf = 1;
     }
     if (nf) bad = 1;  // every writer stores 1
   }

@@ -231,8 +231,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 }
 
 // L2 norm of each output row (src/embedder.rs:83) and optional normalisation (:7-9).
+// A row whose norm is not finite sets *err: an f16 operand of some GEMM overflowed (a
+// T5LayerNorm output |x * gamma| beyond the f16 range) or the weights hold non-finite values.
 __global__ __launch_bounds__(256) void rownorm_kernel(float* __restrict__ y, float* __restrict__ norm,
-                                                      int T, int P, int normalize) {
+                                                      int T, int P, int normalize, unsigned* err) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int lane = threadIdx.x & 63;
@@ -242,6 +244,7 @@ __global__ __launch_bounds__(256) void rownorm_kernel(float* __restrict__ y, flo
   ss = wave_sum(ss);
   const float n = sqrtf(ss);
   if (lane == 0 && norm) norm[t] = n;
+  if (lane == 0 && err && !__builtin_isfinite(n)) *(volatile unsigned*)err = 1u;  // every writer stores 1
   if (normalize)
     for (int i = lane; i < P; i += 64) r[i] = r[i] / n;
 }
@@ -281,9 +284,9 @@ hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, 
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec, rec_stride);
   return hipGetLastError();
 }
-hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s) {
+hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s, unsigned* err) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize);
+  hipLaunchKernelGGL(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize, err);
   return hipGetLastError();
 }
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s) {

@@ -186,8 +186,9 @@ struct t5h_model {
   // The buffers every launch of a forward reads and writes: carved from `ws`, or from the
   // library's fixed per-device array for t5h_encode_device_noalloc (swapped in for that call).
   Workspace w;
-  // Out-of-vocabulary flag in mapped pinned host memory: the embed kernel stores 1 through
-  // err_flag (its device address); the host reads err_host after the stream is synchronised.
+  // Error flags in mapped pinned host memory, written by kernels through err_flag (its device
+  // address) and read by the host after the stream is synchronised: word 0 out-of-vocabulary
+  // ids (embed kernel), word 1 a non-finite output row (row-norm kernel).
   unsigned* err_host = nullptr;
   unsigned* err_flag = nullptr;
   void* scratch = nullptr;  // this device's address of the no-alloc scratch array
@@ -788,7 +789,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
     return rc;
   {
     Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
-    HIP_OK(t5k::launch_rownorm(d_out, d_norm, T, c.proj_dim, normalize, m->stream));
+    HIP_OK(t5k::launch_rownorm(d_out, d_norm, T, c.proj_dim, normalize, m->stream, m->err_flag + 1));
     if (m->prof) {
       ReplayRec& r = m->replay[K_ROWNORM];
       r.type = ReplayRec::ROWNORM;
@@ -867,9 +868,17 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
 int finish_sync(t5h_model* m) {
   HIP_OK(hipStreamSynchronize(m->stream));
   if (m->prof) resolve_timings(m);
-  if (*(volatile unsigned*)m->err_host) {
-    *(volatile unsigned*)m->err_host = 0;
+  volatile unsigned* err = m->err_host;
+  if (err[0]) {
+    err[0] = 0;
+    err[1] = 0;
     return fail(T5H_ERR_INVALID, "token id outside the vocabulary");
+  }
+  if (err[1]) {
+    err[1] = 0;
+    return fail(T5H_ERR_INVALID,
+                "non-finite embedding: an f16 GEMM operand overflowed (a T5LayerNorm output |x * gamma| "
+                "beyond the f16 range) or the weights hold non-finite values");
   }
   return T5H_OK;
 }
@@ -1147,7 +1156,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   HIP_OK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
   if (hipHostMalloc((void**)&m->err_host, 256, hipHostMallocMapped) != hipSuccess)
     return fail(T5H_ERR_NOMEM, "pinned flag allocation failed");
-  *(volatile unsigned*)m->err_host = 0;
+  memset(m->err_host, 0, 256);
   HIP_OK(hipHostGetDevicePointer((void**)&m->err_flag, m->err_host, 0));
   for (int k = 0; k < K_COUNT; k++) m->stats[k].name = kKernelNames[k];
   *out = m.release();
@@ -1396,7 +1405,8 @@ int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) 
       case ReplayRec::EMBED:
         return t5k::launch_embed(r.ids, r.n, r.table, r.fmt, r.vocab, r.D, r.x, m->err_flag, m->stream, r.gamma,
                                  r.eps, r.xn, r.rec, r.rec_stride);
-      case ReplayRec::ROWNORM: return t5k::launch_rownorm(r.y, r.norm, r.n, r.P, r.normalize, m->stream);
+      case ReplayRec::ROWNORM:
+        return t5k::launch_rownorm(r.y, r.norm, r.n, r.P, r.normalize, m->stream, m->err_flag + 1);
       case ReplayRec::RMSNORM:
         return t5k::launch_rmsnorm(r.x, r.gamma, r.xn, r.n, r.D, r.eps, m->stream, r.rec, r.rec_stride);
       default: return hipErrorInvalidValue;
