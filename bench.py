@@ -492,6 +492,9 @@ def main() -> None:
     ap.add_argument("--queries", type=int, default=1000, help="cfg3: number of timed queries")
     ap.add_argument("--rotate", type=int, default=8, help="cfg3: model replicas cycled (MALL defeat)")
     ap.add_argument("--no-query", action="store_true", help="cfg2: leave out the cfg3 query object")
+    ap.add_argument("--numerics", default="default", choices=["default", "hybrid"],
+                    help="batched workloads: t5h_set_numerics mode (hybrid: the hybrid-dequant "
+                         "feature's Q8_K x Q4_K FFN and projection)")
     ap.add_argument("--score-n", type=int, default=1 << 20, help="score: residual rows")
     ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
     ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
@@ -536,6 +539,8 @@ def main() -> None:
     img = synth.make_model(cfg, seed=args.seed, layout="hybrid" if args.workload == "cfg5" else "q4k")
     log(f"[bench] model built in {time.perf_counter() - t0:.1f}s ({len(img) / 1e6:.1f} MB GGUF)")
     model = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
+    if args.numerics == "hybrid":
+        model.set_numerics(1)
     ids, cu = synth.ragged_batch(n_seqs, lo, hi, cfg["vocab_size"], seed=1000 + args.seed)
     T = int(cu[-1])
     dev = torch.device("cuda:0")
@@ -595,6 +600,10 @@ def main() -> None:
                 "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6,
                 "share_of_step": dom["ms_per_step"] / sum(v["ms_per_step"] for v in kernels.values()),
                 "counters": counters}
+    if args.numerics == "hybrid" and dom_name in ("gemm_ffn_gate_up", "gemm_proj"):
+        # the hybrid FFN runs integer dot products on the vector ALUs, not on the matrix cores
+        roofline.update({"kernel": f"{dom_name} (Q8_K quantize + Q4_K x Q8_K v_dot4_i32_i8)", "bound": "valu",
+                         "unit": "TOP/s", "peak": None, "frac": None})
 
     base = None
     if not args.no_cpu_baseline:
@@ -610,10 +619,10 @@ def main() -> None:
     line = {
         "metric": METRIC, "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "vs_baseline": None, "dtype": "f16" if args.numerics == "default" else "f16+int8", "data": "synthetic",
         "config": {"workload": f"{args.workload}: {desc}", "global_batch": n_seqs, "seq_len": pad,
                    "tokens_per_step": T, "weights": "random-init N(0,0.02^2), Q4_K by the quantize tool's scale/min search (t5h_quantize_q4k); f32 embeddings and norms",
-                   "parallelism": "single GPU"},
+                   "numerics": args.numerics, "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": base, "kernels": kernels,
     }
     if query is not None:

@@ -124,6 +124,19 @@ int t5h_embed_batch(t5h_model* model, const uint32_t* ids, const int32_t* doc_of
                     int32_t max_len, int32_t stride, float* out, int32_t* kept_index,
                     int32_t* kept_offsets);
 
+/* ---- numerics of the FFN and the projection ----
+ * T5H_NUMERICS_DEFAULT: the `t5-quantized` numerics -- Q4_K weights dequantized exactly,
+ *   activations and weights rounded to f16 for the MFMAs (f32 accumulation), tanh gelu.
+ * T5H_NUMERICS_HYBRID: the `hybrid-dequant` feature's (src/quantized_t5.rs:18-21,233-244) --
+ *   wi_0 / wi_1 and the final projection take f32 T5LayerNorm outputs quantized to Q8_K
+ *   (candle BlockQ8K::from_float) times Q4_K weights by GGML's integer vec_dot
+ *   (src/fused_matmul.rs:27-59 QTiledOp, :138-177 fused gated gelu with the Pade tanh of
+ *   :128-133); the other linears keep the default numerics.  Needs Q4_K wi_0, wi_1 and
+ *   linear.weight and a gated FFN.  Default: T5H_NUMERICS_DEFAULT. */
+#define T5H_NUMERICS_DEFAULT 0
+#define T5H_NUMERICS_HYBRID 1
+int t5h_set_numerics(t5h_model* model, int32_t mode);
+
 /* ---- offline weight quantization (host only, no device needed) ---- */
 
 /* f32 values -> GGML Q4_K super-blocks (144 bytes per 256 values): the quantize tool's
@@ -133,6 +146,15 @@ int t5h_embed_batch(t5h_model* model, const uint32_t* ids, const int32_t* doc_of
 int t5h_quantize_q4k(const float* x, int64_t n_values, uint8_t* out, int32_t threads);
 
 /* ---- test hooks (teacher-forced parity checks) ---- */
+
+/* BlockQ8K::from_float on the device (src/fused_matmul.rs:36-41): x[rows][cols] f32 (cols % 256
+ * == 0, <= 1024) -> rows * cols / 256 blocks of 292 bytes {f32 d, i8 qs[256], i16 bsums[16]}.
+ * Host buffers. */
+int t5h_q8k_quantize(int32_t hip_device, const float* x, int32_t rows, int32_t cols, uint8_t* blocks);
+/* out[T][N] = vec_dot(w row n, x8 row t) for Q4_K rows w[N][K] and Q8_K rows x8[T][K]
+ * (BlockQ4K::vec_dot, src/fused_matmul.rs:55; N % 64 == 0).  Host buffers. */
+int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const uint8_t* x8, int32_t T,
+                       int32_t K, float* out);
 
 /* Q4_K -> f32, bit-exact with candle BlockQ4K::to_float (reached from
  * src/quantized_t5.rs:44).  blocks/out are HOST buffers. */

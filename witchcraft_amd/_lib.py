@@ -19,6 +19,9 @@ T5H_ERR_HIP = -3
 T5H_ERR_NOMEM = -4
 T5H_ERR_NODEVICE = -5
 
+T5H_NUMERICS_DEFAULT = 0
+T5H_NUMERICS_HYBRID = 1
+
 
 class T5HConfig(C.Structure):
     _fields_ = [
@@ -57,6 +60,9 @@ SIGNATURES = {
                                 C.POINTER(C.c_int32)]),
     "t5h_embed_batch": (C.c_int, [_vp, _u32p, _i32p, C.c_int32, C.c_int32, C.c_int32, _f32p, _i32p, _i32p]),
     "t5h_quantize_q4k": (C.c_int, [_f32p, C.c_int64, _u8p, C.c_int32]),
+    "t5h_set_numerics": (C.c_int, [_vp, C.c_int32]),
+    "t5h_q8k_quantize": (C.c_int, [C.c_int32, _f32p, C.c_int32, C.c_int32, _u8p]),
+    "t5h_q4k_q8k_matmul": (C.c_int, [C.c_int32, _u8p, C.c_int32, _u8p, C.c_int32, C.c_int32, _f32p]),
     "t5h_q4k_dequant_f32": (C.c_int, [_u8p, C.c_size_t, _f32p, C.c_int]),
     "t5h_matmul_t": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _f32p]),
     "t5h_matmul_argmax": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _u32p]),

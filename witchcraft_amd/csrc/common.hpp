@@ -181,4 +181,13 @@ hipError_t launch_embed_batch(const float* win, const int4* docs, const int* tok
                               int* kept_index, int* kept_offsets, hipStream_t s);
 // Blocks of tokens the embed kernels use for N tokens (block_counts / block_offsets need one more).
 int embed_batch_blocks(int N);
+// Hybrid-dequant numerics (k_q8k.hip): f32 rows [T][D] (T5LayerNorm with gamma first, unless
+// gamma is null) -> GGML Q8_K blocks [T][D/256]; then Q4_K weights [N][K] x Q8_K rows by
+// integer dot products: f32 out [T][ldo] (W1 null) or gelu_pade(W0 row) * (W1 row) as the f16
+// operand [T][N] of the next GEMM (operand order).
+int q8k_bytes_per_row(int D);
+hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, int T, int D, uint8_t* out,
+                               hipStream_t s);
+hipError_t launch_q4k_q8k(const uint8_t* W0, const uint8_t* W1, const uint8_t* X8, int T, int N, int K, float* outf,
+                          int ldo, _Float16* outh, hipStream_t s);
 }  // namespace t5k

@@ -125,7 +125,7 @@ struct Workspace {
 // The arguments of the last launch of each kernel class in a profiled forward, so that
 // t5h_replay_kernel can relaunch it back to back between two events.
 struct ReplayRec {
-  enum Type { NONE, GEMM, GEMV, ATTN, EMBED, ROWNORM, RMSNORM } type = NONE;
+  enum Type { NONE, GEMM, GEMV, ATTN, EMBED, ROWNORM, RMSNORM, HYBRID } type = NONE;
   int epi = 0, wfmt = 0, n = 0;
   GemmArgs ga{};
   t5k::GemmPlan plan{};
@@ -141,6 +141,10 @@ struct ReplayRec {
   float eps = 0.f;
   _Float16* xn = nullptr;
   float* rec = nullptr;
+  // hybrid linear (Q8_K quantize + Q4_K x Q8_K): x, gamma, eps, n (tokens), D; weights, output
+  const uint8_t *hw0 = nullptr, *hw1 = nullptr;
+  uint8_t* x8 = nullptr;
+  int hN = 0, hK = 0, ldo = 0;
 };
 
 struct StagingSlot {
@@ -163,6 +167,7 @@ struct t5h_model {
   int gemm_bn_override = 0;
   int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail, 3 / 4 = all thin
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
+  int numerics = T5H_NUMERICS_DEFAULT;  // t5h_set_numerics
 
   // ---- weights (one device arena) ----
   void* arena = nullptr;
@@ -480,7 +485,40 @@ struct NormLink {
 bool fold_norm(const t5h_model* m, int T) {
   (void)T;
   const int D = m->cfg.d_model;
-  return !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
+  // the hybrid FFN and projection normalise their own f32 input, so no norm is folded there
+  return !m->fold_norm_off && m->numerics == T5H_NUMERICS_DEFAULT && D % 64 == 0 && D <= NORM_REC_MAX_D;
+}
+
+// Hybrid numerics (t5h_set_numerics): the FFN's gate|up and the projection quantize their f32
+// input to Q8_K and use integer Q4_K x Q8_K dot products.  The Q8_K rows live in the attention
+// output buffer `ao`, which is free once the O GEMM has consumed it (checked to fit at
+// t5h_set_numerics).  ln: the T5LayerNorm weight applied first (f32, from the residual x).
+int hybrid_linear(t5h_model* m, int kind, const float* ln, const Linear& W0, const Linear* W1, int T, float* outf,
+                  int ldo) {
+  const t5h_config& c = m->cfg;
+  uint8_t* x8 = (uint8_t*)m->w.ao;
+  Timed t(m, kind, 2.0 * T * W0.N * W0.K * (W1 ? 2 : 1), 0);
+  HIP_OK(t5k::launch_q8k_quantize(m->w.x, ln, c.layer_norm_epsilon, T, c.d_model, x8, m->stream));
+  HIP_OK(t5k::launch_q4k_q8k((const uint8_t*)W0.w, W1 ? (const uint8_t*)W1->w : nullptr, x8, T, W0.N, W0.K, outf, ldo,
+                             W1 ? m->w.hb : nullptr, m->stream));
+  if (m->prof) {
+    ReplayRec& r = m->replay[kind];
+    r.type = ReplayRec::HYBRID;
+    r.x = m->w.x;
+    r.gamma = ln;
+    r.eps = c.layer_norm_epsilon;
+    r.n = T;
+    r.D = c.d_model;
+    r.x8 = x8;
+    r.hw0 = (const uint8_t*)W0.w;
+    r.hw1 = W1 ? (const uint8_t*)W1->w : nullptr;
+    r.hN = W0.N;
+    r.hK = W0.K;
+    r.y = outf;
+    r.ldo = ldo;
+    r.xn = W1 ? m->w.hb : nullptr;
+  }
+  return T5H_OK;
 }
 // Floats per norm record: the GEMV kernels keep one partial sum per 16 columns.
 int rec_stride(const t5h_model* m, int T) { return use_gemv(m, T) ? NORM_REC_GEMV : 16; }
@@ -707,6 +745,10 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
   if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->w.ao, inner, T, m->w.x, D, 0, nullptr, fold ? &on : nullptr)))
     return rc;
   const float* nw1 = nullptr;
+  if (m->numerics == T5H_NUMERICS_HYBRID) {
+    if ((rc = hybrid_linear(m, K_GEMM_GATE_UP, Ly.ln1, Ly.wi0, &Ly.wi1, T, nullptr, 0))) return rc;
+    return gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, D, 0, nullptr, nullptr);
+  }
   if (!fold) {
     nw1 = prenorm(m, Ly.ln1, T, rc);
     if (rc) return rc;
@@ -778,15 +820,19 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
   }
   const float* nwf = nullptr;
   NormLink pn;
-  if (fold) {
-    pn.rec = m->w.rec0;
+  if (m->numerics == T5H_NUMERICS_HYBRID) {
+    if ((rc = hybrid_linear(m, K_GEMM_PROJ, m->final_ln, m->proj, nullptr, T, d_out, c.proj_dim))) return rc;
   } else {
-    nwf = prenorm(m, m->final_ln, T, rc);
-    if (rc) return rc;
+    if (fold) {
+      pn.rec = m->w.rec0;
+    } else {
+      nwf = prenorm(m, m->final_ln, T, rc);
+      if (rc) return rc;
+    }
+    if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->w.xn, c.d_model, T, d_out, c.proj_dim, 0, nwf,
+                   fold ? &pn : nullptr)))
+      return rc;
   }
-  if ((rc = gemm(m, K_GEMM_PROJ, EPI_F32, m->proj, nullptr, m->w.xn, c.d_model, T, d_out, c.proj_dim, 0, nwf,
-                 fold ? &pn : nullptr)))
-    return rc;
   {
     Timed t(m, K_ROWNORM, 0, (double)T * c.proj_dim * 8);
     HIP_OK(t5k::launch_rownorm(d_out, d_norm, T, c.proj_dim, normalize, m->stream, m->err_flag + 1));
@@ -1366,14 +1412,82 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   const Layer& Ly = m->layers[layer];
   const size_t bytes = (size_t)T * c.d_model * 4;
   HIP_OK(hipMemcpyAsync(m->w.x, x, bytes, hipMemcpyHostToDevice, m->stream));
-  HIP_OK(t5k::launch_f32_to_f16(m->w.x, m->w.xn, (size_t)T * c.d_model, c.d_model, m->stream));
   m->batched_only = mode == 1;
-  rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn, c.d_model, T, m->w.hb, c.d_ff);
+  if (m->numerics == T5H_NUMERICS_HYBRID) {
+    rc = hybrid_linear(m, K_GEMM_GATE_UP, nullptr, Ly.wi0, &Ly.wi1, T, nullptr, 0);
+  } else {
+    HIP_OK(t5k::launch_f32_to_f16(m->w.x, m->w.xn, (size_t)T * c.d_model, c.d_model, m->stream));
+    rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn, c.d_model, T, m->w.hb, c.d_ff);
+  }
   if (!rc) rc = gemm(m, K_GEMM_WO, EPI_F32, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, c.d_model);
   m->batched_only = false;
   if (rc) return rc;
   HIP_OK(hipMemcpyAsync(y, m->w.x, bytes, hipMemcpyDeviceToHost, m->stream));
   return finish_sync(m);
+}
+
+int t5h_set_numerics(t5h_model* m, int32_t mode) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  if (mode == T5H_NUMERICS_DEFAULT) {
+    HIP_OK(hipStreamSynchronize(m->stream));
+    m->numerics = mode;
+    return T5H_OK;
+  }
+  if (mode != T5H_NUMERICS_HYBRID) return fail(T5H_ERR_INVALID, "unknown numerics mode");
+  const t5h_config& c = m->cfg;
+  if (!c.feed_forward_gated) return fail(T5H_ERR_INVALID, "hybrid numerics: the FFN must be gated-gelu");
+  for (const Layer& Ly : m->layers)
+    if (Ly.wi0.fmt != WF_Q4K || Ly.wi1.fmt != WF_Q4K)
+      return fail(T5H_ERR_INVALID, "hybrid numerics: wi_0 / wi_1 must be Q4_K (QGatedMatMul)");
+  if (m->proj.fmt != WF_Q4K) return fail(T5H_ERR_INVALID, "hybrid numerics: linear.weight must be Q4_K (QTiledOp)");
+  if (c.d_model % QK_K || c.d_model > 1024 || c.d_ff % 64 || c.proj_dim % 64)
+    return fail(T5H_ERR_INVALID, "hybrid numerics: needs d_model % 256 == 0 (<= 1024), d_ff and proj_dim % 64 == 0");
+  if ((size_t)t5k::q8k_bytes_per_row(c.d_model) > (size_t)m->inner * 2)
+    return fail(T5H_ERR_INVALID, "hybrid numerics: Q8_K rows do not fit the attention output buffer");
+  HIP_OK(hipStreamSynchronize(m->stream));
+  m->numerics = mode;
+  return T5H_OK;
+}
+
+int t5h_q8k_quantize(int32_t hip_device, const float* x, int32_t rows, int32_t cols, uint8_t* blocks) {
+  if (rows < 0 || cols <= 0 || cols % QK_K || cols > 1024) return fail(T5H_ERR_INVALID, "q8k_quantize: bad shape");
+  if (rows == 0) return T5H_OK;
+  if (!x || !blocks) return fail(T5H_ERR_INVALID, "q8k_quantize: NULL buffer");
+  HIP_OK(hipSetDevice(hip_device));
+  const size_t xb = (size_t)rows * cols * 4, ob = (size_t)rows * t5k::q8k_bytes_per_row(cols);
+  void* d = nullptr;
+  if (hipMalloc(&d, align256(xb) + ob) != hipSuccess) return fail(T5H_ERR_NOMEM, "q8k_quantize buffers");
+  uint8_t* dx = (uint8_t*)d;
+  hipError_t e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = t5k::launch_q8k_quantize((const float*)dx, nullptr, 0.f, rows, cols, dx + align256(xb), nullptr);
+  if (e == hipSuccess) e = hipMemcpy(blocks, dx + align256(xb), ob, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("q8k_quantize: ") + hipGetErrorString(e));
+  return T5H_OK;
+}
+
+int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const uint8_t* x8, int32_t T, int32_t K,
+                       float* out) {
+  if (N < 0 || T < 0 || K <= 0 || K % QK_K || N % 64) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: bad shape");
+  if (N == 0 || T == 0) return T5H_OK;
+  if (!w || !x8 || !out) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: NULL buffer");
+  HIP_OK(hipSetDevice(hip_device));
+  const size_t wb = (size_t)N * K / QK_K * Q4K_BYTES, x8b = (size_t)T * t5k::q8k_bytes_per_row(K),
+               ob = (size_t)T * N * 4;
+  void* d = nullptr;
+  if (hipMalloc(&d, align256(wb) + align256(x8b) + ob) != hipSuccess)
+    return fail(T5H_ERR_NOMEM, "q4k_q8k_matmul buffers");
+  uint8_t* dw = (uint8_t*)d;
+  uint8_t* dx = dw + align256(wb);
+  float* dout = (float*)(dx + align256(x8b));
+  hipError_t e = hipMemcpy(dw, w, wb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dx, x8, x8b, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = t5k::launch_q4k_q8k(dw, nullptr, dx, T, N, K, dout, N, nullptr, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(out, dout, ob, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("q4k_q8k_matmul: ") + hipGetErrorString(e));
+  return T5H_OK;
 }
 
 int t5h_set_profiling(t5h_model* m, int32_t on) {
@@ -1409,6 +1523,11 @@ int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) 
         return t5k::launch_rownorm(r.y, r.norm, r.n, r.P, r.normalize, m->stream, m->err_flag + 1);
       case ReplayRec::RMSNORM:
         return t5k::launch_rmsnorm(r.x, r.gamma, r.xn, r.n, r.D, r.eps, m->stream, r.rec, r.rec_stride);
+      case ReplayRec::HYBRID: {
+        const hipError_t e = t5k::launch_q8k_quantize(r.x, r.gamma, r.eps, r.n, r.D, r.x8, m->stream);
+        if (e != hipSuccess) return e;
+        return t5k::launch_q4k_q8k(r.hw0, r.hw1, r.x8, r.n, r.hN, r.hK, r.y, r.ldo, r.xn, m->stream);
+      }
       default: return hipErrorInvalidValue;
     }
   };

@@ -148,6 +148,11 @@ class T5EncoderModel:
         check(lib.t5h_embed_batch(self._h, ids, offs, len(docs), max_len, stride, out, kept, koff))
         return [(out[koff[d]:koff[d + 1]], kept[koff[d]:koff[d + 1]]) for d in range(len(docs))]
 
+    def set_numerics(self, mode: int) -> None:
+        """T5H_NUMERICS_DEFAULT (t5-quantized) or T5H_NUMERICS_HYBRID (hybrid-dequant: Q8_K x Q4_K
+        integer dot products for wi_0 / wi_1 and the projection, Pade gelu)."""
+        check(lib.t5h_set_numerics(self._h, int(mode)))
+
     # ---- test hooks ----
     def layer_forward(self, layer: int, x: np.ndarray, cu_seqlens: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)
@@ -211,6 +216,26 @@ class T5ModelBuilder:
             raise FileNotFoundError("failed to get bytes for MODEL") from e
         dev = device if isinstance(device, int) else 0
         return T5EncoderModel(model_bytes, self.config, dev)
+
+
+def q8k_quantize(x: np.ndarray, hip_device: int = 0) -> np.ndarray:
+    """BlockQ8K::from_float on the GPU (src/fused_matmul.rs:36-41): f32 [rows, cols]
+    (cols % 256 == 0) -> uint8 [rows, cols / 256 * 292]."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    out = np.empty((rows, cols // 256 * 292), np.uint8)
+    check(lib.t5h_q8k_quantize(hip_device, x, rows, cols, out))
+    return out
+
+
+def q4k_q8k_matmul(w: np.ndarray, x8: np.ndarray, K: int, hip_device: int = 0) -> np.ndarray:
+    """out[t, n] = BlockQ4K::vec_dot(w[n], x8[t]) on the GPU: Q4_K rows [N, K/256*144] and
+    Q8_K rows [T, K/256*292] -> f32 [T, N]."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1, K // 256 * 144)
+    x8 = np.ascontiguousarray(x8, np.uint8).reshape(-1, K // 256 * 292)
+    out = np.empty((x8.shape[0], w.shape[0]), np.float32)
+    check(lib.t5h_q4k_q8k_matmul(hip_device, w, w.shape[0], x8, x8.shape[0], K, out))
+    return out
 
 
 class Embedder:
