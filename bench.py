@@ -423,6 +423,74 @@ def score_bench(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def embed_bench(args) -> None:
+    """Embedder::embed over a batch of documents (src/embedder.rs:22-103, called once per
+    document by Gatherer::next, src/lib.rs:930-934): `--embed-docs` documents of U[10, 5000]
+    token ids, windows of 2048 overlapping by 256.  The value is document tokens/s of one
+    t5h_embed_batch call (every window of every document in one packed encode; window sums,
+    MIN_NORM filter and compaction on the GPU), host buffers in and out, so the PCIe copies of
+    the ids and the kept rows are inside the timed region.  Reported beside it: the same
+    documents through t5h_embed_ids one after another, as the reference's loop runs them."""
+    from witchcraft_amd import synth
+    from witchcraft_amd.encoder import T5EncoderModel
+
+    cfg = dict(synth.XTR_BASE)
+    img = synth.make_model(cfg, seed=args.seed)
+    model = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
+    r = np.random.default_rng(3000 + args.seed)
+    lens = r.integers(10, 5001, args.embed_docs)
+    docs = [r.integers(1, cfg["vocab_size"], n).astype(np.uint32) for n in lens]
+    ntok = int(lens.sum())
+    model.embed_batch(docs)  # warm-up: workspace and staging sized once
+    t_batch = []
+    for _ in range(max(3, args.steps // 4)):
+        t = time.perf_counter()
+        res = model.embed_batch(docs)
+        t_batch.append(time.perf_counter() - t)
+    tb = float(np.median(t_batch))
+    kept = sum(k.size for _, k in res)
+    t = time.perf_counter()
+    for d in docs:
+        model.embed_ids(d)
+    tl = time.perf_counter() - t
+    log(f"[bench] embed: {len(docs)} documents, {ntok} tokens: batch {tb * 1e3:.1f} ms "
+        f"({ntok / tb:,.0f} tokens/s), one at a time {tl * 1e3:.1f} ms ({ntok / tl:,.0f} tokens/s), kept {kept}")
+    kernels = kernel_table(model, lambda: model.embed_batch(docs), 2)
+    model.close()
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle.torch_port import TorchCpuEncoder
+        info = cpu_info()
+        port = TorchCpuEncoder(img, cfg, threads=info["threads"])
+        t0, done = time.perf_counter(), 0
+        for d in docs:
+            n, k = d.size, 0
+            while True:  # the reference's windows: start k * 1792 until a window reaches the end
+                port.forward(d[k * 1792:min(k * 1792 + 2048, n)])
+                if k * 1792 + 2048 >= n:
+                    break
+                k += 1
+            done += n
+            if time.perf_counter() - t0 > min(args.cpu_budget, 20.0):
+                break
+        cpu = time.perf_counter() - t0
+        base = {"value": done / cpu, "unit": "tokens/s", "cores": info["threads"], "kind": "port",
+                "sample": f"{done} document tokens, windows encoded one by one (batch-1) on torch CPU GEMMs "
+                          f"(f32 dequantize-at-load path); CPU {info['model']}"}
+    line = {
+        "metric": "XTR-base Q4_K document embedding tokens/sec (t5h_embed_batch, windows 2048/256)",
+        "value": ntok / tb, "unit": "tokens/s", "n_gpus": 1, "steps": len(t_batch), "warmup": 1,
+        "ms_per_step": tb * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"embed: {len(docs)} documents of U[10, 5000] token ids, {ntok} tokens",
+                   "kept_rows": kept, "one_at_a_time_tokens_per_s": ntok / tl,
+                   "batch_over_one_at_a_time": tl / tb, "parallelism": "single GPU",
+                   "note": "host buffers in and out: PCIe copies inside the timed region"},
+        "cpu_baseline": base, "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def codec_bench(args) -> None:
     """Chunk-embedding codec after the encoder (src/lib.rs:1091 embeddings_to_packed per chunk,
     decoded at :712,1178,1296): a batch of `--codec-docs` matrices of L ~ U[64, 512] unit
@@ -485,7 +553,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + ["score", "codec"])
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + ["score", "codec", "embed"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -499,6 +567,7 @@ def main() -> None:
     ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
     ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
     ap.add_argument("--codec-docs", type=int, default=256, help="codec: chunks per batch")
+    ap.add_argument("--embed-docs", type=int, default=64, help="embed: documents per batch")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 10 times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -526,6 +595,9 @@ def main() -> None:
         return
     if args.workload == "codec":
         codec_bench(args)
+        return
+    if args.workload == "embed":
+        embed_bench(args)
         return
 
     import torch
