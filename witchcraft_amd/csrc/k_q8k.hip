@@ -14,10 +14,11 @@
 //    iscale = -128 / v, q = min(127, round(iscale * x)) with halves away from zero, d = 1 / iscale,
 //    bsums = sums of 16 consecutive q; an all-zero block gives d = 0 and q = 0.  Bit-exact with
 //    BlockQ8K::from_float on the same f32 input.
-//  * q4k_q8k_kernel: tile of 64 weight rows x 16 tokens per 256-thread workgroup; the Q4_K
-//    rows and Q8_K token blocks of each 256-wide K block are staged in LDS; each thread forms
-//    the integer sums of 32-value sub-blocks with v_dot4_i32_i8 (exact), weights them with the
-//    6-bit scales in int32 (exact), and combines per block in f32 as vec_dot does:
+//  * q4k_q8k_kernel: tile of 128 weight rows x 32 tokens per 256-thread workgroup (4 rows x 4
+//    tokens per thread); the Q4_K rows and Q8_K token blocks of each 256-wide K block are
+//    staged in LDS; each thread forms the integer sums of 32-value sub-blocks with
+//    v_dot4_i32_i8 (exact), weights them with the 6-bit scales in int32 (exact), and combines
+//    per block in f32 as vec_dot does:
 //    + f16(d) * d8 * sum_j sc_j (q4 . q8)_j  - f16(dmin) * d8 * sum_j m_j (bsum_2j + bsum_2j+1).
 //    GGML's generic C code keeps eight lane partials of the first term and x86 builds use AVX2
 //    lanes: the float combination order is implementation-defined in the reference too.
@@ -114,98 +115,138 @@ __device__ __forceinline__ float gelu_pade(float g) {
   return 0.5f * g * (1.0f + fast_tanh_pade(0.7978845608f * g * (1.0f + 0.044715f * g * g)));
 }
 
-constexpr int QR = 64, QT = 16;  // weight rows x tokens per workgroup
+constexpr int QR = 128, QT = 32;  // weight rows x tokens per workgroup
 
+// Workgroup of 256 threads: thread (rg = tid / 8, tg = tid % 8) owns weight rows 4 rg .. 4 rg + 3
+// and tokens 4 tg .. 4 tg + 3 (16 outputs per weight matrix).  Per 256-wide K block the rows'
+// Q4_K blocks and the tokens' Q8_K blocks are staged in LDS; per pair of 32-value sub-blocks a
+// thread reads each of its rows' 32 nibble bytes and each of its tokens' 64 q8 bytes once
+// (16-byte reads) and issues 16 v_dot4_i32_i8 per (row, token).
 template <int G>  // 1: plain, 2: gated (W0 gate, W1 up)
 __global__ __launch_bounds__(256) void q4k_q8k_kernel(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1,
                                                       const uint8_t* __restrict__ X8, int T, int N, int K,
                                                       float* __restrict__ outf, int ldo, _Float16* __restrict__ outh) {
-  __shared__ uint32_t wsh[G][QR * Q4K_BYTES / 4];
-  __shared__ uint32_t xsh[QT * Q8K_BYTES / 4];
-  const int tid = threadIdx.x, r = tid >> 2, tq = tid & 3;
+  __shared__ __attribute__((aligned(16))) uint32_t wsh[G][QR * Q4K_BYTES / 4];
+  // Q8_K blocks in LDS padded to 76 words so the q8 bytes start 16-byte aligned: d at word 0,
+  // q8 at words 4 .. 67, bsums at words 68 .. 75
+  constexpr int XW = 76;
+  __shared__ __attribute__((aligned(16))) uint32_t xsh[QT * XW];
+  const int tid = threadIdx.x, rg = tid >> 3, tg = tid & 7;
   const int n0 = blockIdx.x * QR, t0 = blockIdx.y * QT;
   const int kb_n = K / QK_K;
-  float accd[G][4], accm[G][4];
+  float accd[G][4][4], accm[G][4][4];
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) accd[g][j] = accm[g][j] = 0.f;
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) accd[g][r][j] = accm[g][r][j] = 0.f;
   const uint8_t* Wg[2] = {W0, W1};
 
   for (int kb = 0; kb < kb_n; kb++) {
-    // stage the 64 rows' Q4_K blocks and the 16 tokens' Q8_K blocks of this K block
 #pragma unroll
     for (int g = 0; g < G; g++)
       for (int i = tid; i < QR * Q4K_BYTES / 4; i += 256) {
         const int row = i / (Q4K_BYTES / 4), w = i % (Q4K_BYTES / 4);
-        wsh[g][i] = reinterpret_cast<const uint32_t*>(Wg[g] + ((size_t)(n0 + row) * kb_n + kb) * Q4K_BYTES)[w];
+        wsh[g][i] = n0 + row < N
+                        ? reinterpret_cast<const uint32_t*>(Wg[g] + ((size_t)(n0 + row) * kb_n + kb) * Q4K_BYTES)[w]
+                        : 0u;
       }
     for (int i = tid; i < QT * Q8K_BYTES / 4; i += 256) {
       const int tok = i / (Q8K_BYTES / 4), w = i % (Q8K_BYTES / 4);
-      xsh[i] = t0 + tok < T ? reinterpret_cast<const uint32_t*>(X8 + ((size_t)(t0 + tok) * kb_n + kb) * Q8K_BYTES)[w]
-                            : 0u;
+      xsh[tok * XW + (w ? w + 3 : 0)] =
+          t0 + tok < T ? reinterpret_cast<const uint32_t*>(X8 + ((size_t)(t0 + tok) * kb_n + kb) * Q8K_BYTES)[w] : 0u;
     }
     __syncthreads();
+    // per token: d8 and the 16 bsums of this block
+    float d8[4];
+    int bsp[4][8];  // bsum_2j + bsum_2j+1
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t* xb = &xsh[(4 * tg + j) * XW];
+      d8[j] = __uint_as_float(xb[0]);
+      const int16_t* bs = reinterpret_cast<const int16_t*>(xb + 68);
+#pragma unroll
+      for (int k = 0; k < 8; k++) bsp[j][k] = bs[2 * k] + bs[2 * k + 1];
+    }
 #pragma unroll
     for (int g = 0; g < G; g++) {
-      const uint32_t* blk = &wsh[g][r * (Q4K_BYTES / 4)];
-      const float d4 = f16_bits_to_f32(blk[0] & 0xffff), dmin4 = f16_bits_to_f32(blk[0] >> 16);
-      // get_scale_min_k4 over the 12 scale bytes (words 1..3)
-      const uint8_t* sb = reinterpret_cast<const uint8_t*>(blk + 1);
-      int sc[8], mn[8];
+      int aux[4][4];
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        if (j < 4) {
-          sc[j] = sb[j] & 63;
-          mn[j] = sb[j + 4] & 63;
-        } else {
-          sc[j] = (sb[j + 4] & 15) | ((sb[j - 4] >> 6) << 4);
-          mn[j] = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4);
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) aux[r][j] = 0;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {  // sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles)
+        uint4 q8[4][4];             // token j: q8 bytes 64c .. 64c + 63
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int v = 0; v < 4; v++)
+            q8[j][v] = *reinterpret_cast<const uint4*>(&xsh[(4 * tg + j) * XW + 4 + 16 * c + 4 * v]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t* blk = &wsh[g][(4 * rg + r) * (Q4K_BYTES / 4)];
+          const uint8_t* sb = reinterpret_cast<const uint8_t*>(blk + 1);
+          int sc0, sc1;
+          if (c < 2) {
+            sc0 = sb[2 * c] & 63;
+            sc1 = sb[2 * c + 1] & 63;
+          } else {
+            sc0 = (sb[2 * c + 4] & 15) | ((sb[2 * c - 4] >> 6) << 4);
+            sc1 = (sb[2 * c + 5] & 15) | ((sb[2 * c - 3] >> 6) << 4);
+          }
+          const uint4 qa = *reinterpret_cast<const uint4*>(blk + 4 + 8 * c);
+          const uint4 qb = *reinterpret_cast<const uint4*>(blk + 8 + 8 * c);
+          const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const uint32_t q8w[16] = {q8[j][0].x, q8[j][0].y, q8[j][0].z, q8[j][0].w, q8[j][1].x, q8[j][1].y,
+                                      q8[j][1].z, q8[j][1].w, q8[j][2].x, q8[j][2].y, q8[j][2].z, q8[j][2].w,
+                                      q8[j][3].x, q8[j][3].y, q8[j][3].z, q8[j][3].w};
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int w = 0; w < 8; w++) {
+              lo = __builtin_amdgcn_sdot4((int)(qw[w] & 0x0f0f0f0fu), (int)q8w[w], lo, false);
+              hi = __builtin_amdgcn_sdot4((int)((qw[w] >> 4) & 0x0f0f0f0fu), (int)q8w[8 + w], hi, false);
+            }
+            aux[r][j] += sc0 * lo + sc1 * hi;
+          }
         }
       }
-      int aux[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int sbk = 0; sbk < 8; sbk++) {
-        const int c = sbk >> 1;
-        uint32_t q4[8];
+      for (int r = 0; r < 4; r++) {
+        const uint32_t* blk = &wsh[g][(4 * rg + r) * (Q4K_BYTES / 4)];
+        const float d4 = f16_bits_to_f32(blk[0] & 0xffff), dmin4 = f16_bits_to_f32(blk[0] >> 16);
+        const uint8_t* sb = reinterpret_cast<const uint8_t*>(blk + 1);
+        int mn[8];
 #pragma unroll
-        for (int w = 0; w < 8; w++) {
-          const uint32_t b = blk[4 + 8 * c + w];  // nibble bytes qs[32c .. 32c + 31]
-          q4[w] = (sbk & 1) ? (b >> 4) & 0x0f0f0f0fu : b & 0x0f0f0f0fu;
-        }
+        for (int k = 0; k < 8; k++) mn[k] = k < 4 ? sb[k + 4] & 63 : (sb[k + 4] >> 4) | ((sb[k] >> 6) << 4);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const uint32_t* q8 = &xsh[(4 * tq + j) * (Q8K_BYTES / 4) + 1 + 8 * sbk];
-          int isum = 0;
+          int sumi = 0;
 #pragma unroll
-          for (int w = 0; w < 8; w++) isum = __builtin_amdgcn_sdot4((int)q4[w], (int)q8[w], isum, false);
-          aux[j] += sc[sbk] * isum;
+          for (int k = 0; k < 8; k++) sumi += bsp[j][k] * mn[k];
+          accd[g][r][j] += (d4 * d8[j]) * (float)aux[r][j];
+          accm[g][r][j] -= (dmin4 * d8[j]) * (float)sumi;
         }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t* xb = &xsh[(4 * tq + j) * (Q8K_BYTES / 4)];
-        const float d8 = __uint_as_float(xb[0]);
-        const int16_t* bs = reinterpret_cast<const int16_t*>(xb + 65);
-        int sumi = 0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) sumi += bs[k] * mn[k / 2];
-        accd[g][j] += (d4 * d8) * (float)aux[j];
-        accm[g][j] -= (dmin4 * d8) * (float)sumi;
       }
     }
     __syncthreads();
   }
-  const int n = n0 + r;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int t = t0 + 4 * tq + j;
-    if (t >= T) continue;
-    if constexpr (G == 1) {
-      outf[(size_t)t * ldo + n] = accm[0][j] + accd[0][j];
-    } else {
-      const float gate = accm[0][j] + accd[0][j], up = accm[1][j] + accd[1][j];
-      outh[tiled_index(t, n, N)] = (_Float16)(gelu_pade(gate) * up);
+  for (int r = 0; r < 4; r++) {
+    const int n = n0 + 4 * rg + r;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int t = t0 + 4 * tg + j;
+      if (t >= T || n >= N) continue;
+      if constexpr (G == 1) {
+        outf[(size_t)t * ldo + n] = accm[0][r][j] + accd[0][r][j];
+      } else {
+        const float gate = accm[0][r][j] + accd[0][r][j], up = accm[1][r][j] + accd[1][r][j];
+        outh[tiled_index(t, n, N)] = (_Float16)(gelu_pade(gate) * up);
+      }
     }
   }
 }
@@ -226,8 +267,8 @@ hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, in
 hipError_t launch_q4k_q8k(const uint8_t* W0, const uint8_t* W1, const uint8_t* X8, int T, int N, int K, float* outf,
                           int ldo, _Float16* outh, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  if (N % QR || K % QK_K || K <= 0) return hipErrorInvalidValue;
-  const dim3 grid(N / QR, (T + QT - 1) / QT);
+  if (N <= 0 || N % 4 || K % QK_K || K <= 0) return hipErrorInvalidValue;
+  const dim3 grid((N + QR - 1) / QR, (T + QT - 1) / QT);
   if (W1) {
     if (!outh) return hipErrorInvalidValue;
     hipLaunchKernelGGL(q4k_q8k_kernel<2>, grid, dim3(256), 0, s, W0, W1, X8, T, N, K, nullptr, 0, outh);

@@ -1469,7 +1469,7 @@ int t5h_q8k_quantize(int32_t hip_device, const float* x, int32_t rows, int32_t c
 
 int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const uint8_t* x8, int32_t T, int32_t K,
                        float* out) {
-  if (N < 0 || T < 0 || K <= 0 || K % QK_K || N % 64) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: bad shape");
+  if (N < 0 || T < 0 || K <= 0 || K % QK_K || N % 4) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: bad shape");
   if (N == 0 || T == 0) return T5H_OK;
   if (!w || !x8 || !out) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: NULL buffer");
   HIP_OK(hipSetDevice(hip_device));
