@@ -91,9 +91,10 @@ __host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]
   _Float16* out;        // [T][H*dkv] in operand order (tiled_index)
-  const int4* work;     // (sequence start, length, first query, 0) per 64-query tile
+  const int4* work;     // (sequence start, length, first query, head) per workgroup; length 0: empty
   const float* lut;     // [H][2*lutw+1] relative bias by (j - i), centred at lutw
   int heads, tpad, lutw;
+  int sat;  // lut[d] = lut[lutw] for d >= sat and lut[-d] = lut[-lutw] (the buckets saturate)
 };
 
 // Device-side helpers ---------------------------------------------------------
@@ -168,10 +169,12 @@ hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int 
 hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, int M, int N, int D, bool bf16_b,
                                 hipStream_t s);
 // Attention work items written from kernel arguments: CAP sequences per launch.
+// Attention work list entries passed by value: item q of entry i is written at
+// work[pos + 8 q] as (start, len, 64 q, head); an entry of length 0 writes `start` empty items.
 struct WorkChunk {
   static constexpr int CAP = 96;
   int n;
-  int start[CAP], len[CAP], wofs[CAP];
+  int start[CAP], len[CAP], head[CAP], pos[CAP];
 };
 hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s);
 // Embedder post-processing over a batch of documents (k_embed.hip): win = packed window outputs,

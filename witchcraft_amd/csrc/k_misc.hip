@@ -255,13 +255,15 @@ __global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restr
   if (i < n) y[tiled_index(i / K, i % K, K)] = (_Float16)x[i];
 }
 
-// Attention work list from by-value arguments (no host staging buffer): item wofs[i] + q of
-// sequence i is (start[i], len[i], 64 q, 0), the layout upload_batch writes.
+// Attention work list from by-value arguments (no host staging buffer), the layout
+// upload_batch writes: item q of entry i at work[pos[i] + 8 q] (its XCD's list), empty items
+// for an entry of length 0.
 __global__ __launch_bounds__(256) void work_list_kernel(t5k::WorkChunk c, int4* __restrict__ work) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= c.n) return;
-  const int L = c.len[i];
-  for (int q = 0; q * 64 < L; q++) work[c.wofs[i] + q] = make_int4(c.start[i], L, q * 64, 0);
+  const int L = c.len[i], n = L ? (L + 63) / 64 : c.start[i];
+  for (int q = 0; q < n; q++)
+    work[c.pos[i] + 8 * q] = L ? make_int4(c.start[i], L, q * 64, c.head[i]) : make_int4(0, 0, 0, 0);
 }
 
 }  // namespace

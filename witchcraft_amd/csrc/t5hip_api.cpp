@@ -156,6 +156,12 @@ struct StagingSlot {
 
 }  // namespace
 
+// One (sequence, head) of the attention work list: its query tiles go to XCD `xcd`, slots
+// slot0, slot0 + 1, ... of that XCD's list.
+struct AttnGroup {
+  int start, len, head, xcd, slot0;
+};
+
 struct t5h_model {
   t5h_config cfg{};
   int device = 0;
@@ -175,10 +181,11 @@ struct t5h_model {
   const void* emb = nullptr;
   int emb_fmt = EMB_F32;
   const float* rel_lut = nullptr;  // [H][2*lutw+1], bias of distance j - i at lutw + j - i
-  int lutw = 0;
+  int lutw = 0, lut_sat = 0;  // lut_sat: |j - i| from which the bias is the LUT's end value
   std::vector<int> order;  // host scratch: sequence order of the attention work list
+  std::vector<AttnGroup> groups;  // host scratch: the attention work plan
   std::vector<int32_t> last_cu;  // cu_seqlens of the batch whose cu / work list are on the device
-  int last_B = -1;
+  int last_B = -1, last_nwork = 0;
   double attn_flops = 0;   // QK^T + PV flops of one attention launch on the current batch, true tokens
   const float* final_ln = nullptr;
   std::vector<Layer> layers;
@@ -587,15 +594,76 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   return T5H_OK;
 }
 
-// Uploads the attention work list through a pinned staging slot: one (start, length, query
-// tile) item per 64 queries of a sequence, so the kernel needs no further lookup.
+// Attention work plan.  One workgroup per (sequence, head, 64 queries); workgroup b runs on
+// XCD b % 8 (workgroups are dealt round-robin), so the list is laid out as 8 interleaved
+// per-XCD lists.  All query tiles of one (sequence, head) go to one XCD, one after another, so
+// that XCD's L2 holds the group's keys and values while its query tiles stream them (2048
+// tokens: 512 KB per group, read by 32 workgroups).  Groups are taken longest sequence first
+// and each goes to the XCD with the least work (query tiles x key tiles) among those whose
+// list stays within ceil(items / 8) + the longest group, which bounds the padding: the lists
+// are padded to the longest one with empty items (length 0), which exit at once.
+int attn_tiles(int L) { return (L + 63) / 64; }
+
+// Upper bound of the work list length (items incl. padding) for T tokens in B sequences of at
+// most max_len tokens.
+int attn_work_cap(const t5h_model* m, int T, int B) {
+  return m->cfg.num_heads * ((T + 63) / 64 + B) + 8 * (attn_tiles(m->cfg.max_seq_len) + 1);
+}
+
+// Calls emit(group) for every (sequence, head) in `order`; returns the slots per XCD.
+template <class Emit>
+int plan_attention(const t5h_model* m, const int32_t* cu, const std::vector<int>& order, int (&xlen)[8],
+                   Emit&& emit) {
+  const int H = m->cfg.num_heads;
+  long long items = 0, load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int maxq = 0;
+  for (int b : order) {
+    items += (long long)H * attn_tiles(cu[b + 1] - cu[b]);
+    maxq = std::max(maxq, attn_tiles(cu[b + 1] - cu[b]));
+  }
+  const long long cap = (items + 7) / 8 + maxq;
+  for (int x = 0; x < 8; x++) xlen[x] = 0;
+  for (int b : order) {
+    const int L = cu[b + 1] - cu[b], nq = attn_tiles(L);
+    if (!nq) continue;
+    for (int h = 0; h < H; h++) {
+      int best = -1;
+      for (int x = 0; x < 8; x++)
+        if (xlen[x] + nq <= cap && (best < 0 || load[x] < load[best])) best = x;
+      emit(AttnGroup{cu[b], L, h, best, xlen[best]});
+      xlen[best] += nq;
+      load[best] += (long long)nq * nq;
+    }
+  }
+  int slots = 0;
+  for (int x = 0; x < 8; x++) slots = std::max(slots, xlen[x]);
+  return slots;
+}
+
+// Longest sequences first into m->order (m->order is the handle's host scratch).
+void order_by_length(t5h_model* m, const int32_t* cu, int B) {
+  m->order.resize(B);
+  for (int b = 0; b < B; b++) m->order[b] = b;
+  std::stable_sort(m->order.begin(), m->order.end(),
+                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+}
+
+// Uploads the attention work list through a pinned staging slot: one (start, length, first
+// query, head) item per workgroup, so the kernel needs no further lookup.
 int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
-  nwork = 0;
-  for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
   // The same batch layout as the previous upload (e.g. a stream of equal-length queries):
   // the device copy of the work list is still current.
-  if (B == m->last_B && std::equal(cu, cu + B + 1, m->last_cu.begin())) return T5H_OK;
+  if (B == m->last_B && std::equal(cu, cu + B + 1, m->last_cu.begin())) {
+    nwork = m->last_nwork;
+    return T5H_OK;
+  }
   m->last_B = -1;
+  order_by_length(m, cu, B);
+  int xlen[8];
+  m->groups.clear();
+  const int slots = plan_attention(m, cu, m->order, xlen, [m](const AttnGroup& g) { m->groups.push_back(g); });
+  nwork = 8 * slots;
+  if (nwork > m->cap_work) return fail(T5H_ERR_INVALID, "internal: attention work list exceeds its capacity");
   StagingSlot& s = m->slots[m->next_slot];
   m->next_slot = (m->next_slot + 1) % 4;
   if (s.used) HIP_OK(hipEventSynchronize(s.done));
@@ -610,24 +678,19 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   }
   if (!s.done) HIP_OK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
   int4* hw = (int4*)s.host;
-  // Longest sequences first (every query tile of a sequence costs ceil(L/64) key tiles), so
-  // the attention grid drains with its cheapest workgroups.
-  m->order.resize(B);
-  for (int b = 0; b < B; b++) m->order[b] = b;
-  std::stable_sort(m->order.begin(), m->order.end(),
-                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
-  int w = 0;
+  for (const AttnGroup& g : m->groups)
+    for (int q = 0; q < attn_tiles(g.len); q++) hw[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * 64, g.head);
+  for (int x = 0; x < 8; x++)
+    for (int q = xlen[x]; q < slots; q++) hw[(size_t)q * 8 + x] = make_int4(0, 0, 0, 0);
   m->attn_flops = 0;
-  for (int b : m->order) {
+  for (int b = 0; b < B; b++)
     m->attn_flops += 4.0 * (double)(cu[b + 1] - cu[b]) * (cu[b + 1] - cu[b]) * m->cfg.d_kv * m->cfg.num_heads;
-    const int L = cu[b + 1] - cu[b];
-    for (int q = 0; q * 64 < L; q++) hw[w++] = make_int4(cu[b], L, q * 64, 0);
-  }
   if (nwork) HIP_OK(hipMemcpyAsync(m->w.work, hw, (size_t)nwork * sizeof(int4), hipMemcpyHostToDevice, m->stream));
   HIP_OK(hipEventRecord(s.done, m->stream));
   s.used = true;
   m->last_cu.assign(cu, cu + B + 1);
   m->last_B = B;
+  m->last_nwork = nwork;
   return T5H_OK;
 }
 
@@ -732,6 +795,7 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     a.heads = c.num_heads;
     a.tpad = m->w.tpad;
     a.lutw = m->lutw;
+    a.sat = m->lut_sat;
     Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
     if (m->prof) {
@@ -774,7 +838,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
 int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
                     float* d_norm, int normalize) {
   int nwork = 0, rc;
-  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  if ((rc = ensure_workspace(m, T, B, attn_work_cap(m, T, B)))) return rc;
   if ((rc = upload_batch(m, cu, B, nwork))) return rc;
   return enqueue_stack(m, d_ids, T, nwork, d_out, d_norm, normalize);
 }
@@ -868,8 +932,9 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
   if (T == 0) return T5H_OK;
   if (!d_ids || !d_out) return fail(T5H_ERR_INVALID, "d_ids/d_out must not be NULL");
   if (!m->scratch) return fail(T5H_ERR_HIP, "no-alloc scratch array is not mapped on this device");
-  int nwork = 0;
-  for (int b = 0; b < B; b++) nwork += (cu[b + 1] - cu[b] + 63) / 64;
+  order_by_length(m, cu, B);
+  int xlen[8];
+  const int nwork = 8 * plan_attention(m, cu, m->order, xlen, [](const AttnGroup&) {});
   const int tpad = workspace_tpad(T);
   Workspace w;
   const size_t need = carve_workspace(m, tpad, nwork, nullptr, w);
@@ -878,28 +943,26 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
                                      std::to_string(need) + " bytes of workspace; the fixed scratch array holds " +
                                      std::to_string((size_t)T5H_NOALLOC_SCRATCH_BYTES));
   carve_workspace(m, tpad, nwork, (uint8_t*)m->scratch, w);
-  // Work list in the order upload_batch uses (longest sequences first); m->order is the
-  // handle's host scratch, reused across calls.
-  m->order.resize(B);
-  for (int b = 0; b < B; b++) m->order[b] = b;
-  std::stable_sort(m->order.begin(), m->order.end(),
-                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+  // The work list of upload_batch, written by kernels from by-value chunks of groups and of
+  // padding runs (length 0, `start` = number of empty slots).
   t5k::WorkChunk ch;
   ch.n = 0;
-  int wofs = 0;
-  for (int i = 0; i < B; i++) {
-    const int b = m->order[i], L = cu[b + 1] - cu[b];
-    if (L == 0) continue;
-    ch.start[ch.n] = cu[b];
-    ch.len[ch.n] = L;
-    ch.wofs[ch.n] = wofs;
-    wofs += (L + 63) / 64;
+  hipError_t herr = hipSuccess;
+  auto add = [&](int start, int len, int head, int pos) {
+    ch.start[ch.n] = start;
+    ch.len[ch.n] = len;
+    ch.head[ch.n] = head;
+    ch.pos[ch.n] = pos;
     if (++ch.n == t5k::WorkChunk::CAP) {
-      HIP_OK(t5k::launch_work_list(ch, w.work, m->stream));
+      if (herr == hipSuccess) herr = t5k::launch_work_list(ch, w.work, m->stream);
       ch.n = 0;
     }
-  }
-  HIP_OK(t5k::launch_work_list(ch, w.work, m->stream));
+  };
+  plan_attention(m, cu, m->order, xlen, [&](const AttnGroup& g) { add(g.start, g.len, g.head, g.slot0 * 8 + g.xcd); });
+  for (int x = 0; x < 8; x++)
+    if (xlen[x] < nwork / 8) add(nwork / 8 - xlen[x], 0, 0, xlen[x] * 8 + x);
+  if (herr == hipSuccess) herr = t5k::launch_work_list(ch, w.work, m->stream);
+  HIP_OK(herr);
   // Run the stack on the scratch workspace without event timing (events would be created).
   const Workspace saved = m->w;
   const bool prof = m->prof;
@@ -941,7 +1004,7 @@ int encode_host(t5h_model* m, const uint32_t* ids, const int32_t* cu, int32_t B,
       return fail(T5H_ERR_INVALID, "token id " + std::to_string(ids[t]) + " at position " +
                                        std::to_string(t) + " outside the vocabulary");
   const int P = m->cfg.proj_dim;
-  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  if ((rc = ensure_workspace(m, T, B, attn_work_cap(m, T, B)))) return rc;
   const size_t ids_b = align256((size_t)T * 4), out_b = (size_t)T * P * 4, norm_b = (size_t)T * 4;
   if ((rc = ensure_io(m, ids_b + out_b + norm_b))) return rc;
   uint8_t* io = (uint8_t*)m->io;
@@ -988,7 +1051,7 @@ int embed_batch_impl(t5h_model* m, const uint32_t* ids, const int32_t* doc_off, 
     for (int k = 0; k < nwin; k++) cu.push_back(cu.back() + std::min(max_len, n - k * step));
   }
   const int W = n_docs ? (int)cu.size() - 1 : 0, T = cu.back();
-  if ((rc = ensure_workspace(m, T, W, (T + 63) / 64 + W))) return rc;
+  if ((rc = ensure_workspace(m, T, W, attn_work_cap(m, T, W)))) return rc;
   // device buffers of the post-processing
   const int nb = t5k::embed_batch_blocks(N);
   size_t off = 0;
@@ -1136,6 +1199,15 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
                                     cfg->relative_attention_max_distance);
       for (int h = 0; h < H; h++) lut[(size_t)h * span + dlt + lutw] = tab[b * H + h];
     }
+    // Distance from which the bucket no longer changes (in either direction), so the bias is
+    // the LUT's end value: the attention kernel skips the bias reads for key tiles that far.
+    auto bucket = [cfg](int dlt) {
+      return rel_bucket(dlt < 0 ? (uint32_t)(-dlt) : 0u, dlt < 0 ? 0u : (uint32_t)dlt,
+                        cfg->relative_attention_num_buckets, cfg->relative_attention_max_distance);
+    };
+    int sat = lutw;
+    while (sat > 1 && bucket(sat - 1) == bucket(lutw) && bucket(-(sat - 1)) == bucket(-lutw)) sat--;
+    m->lut_sat = sat;
   }
   m->layers.resize(cfg->num_layers);
   for (int l = 0; l < cfg->num_layers; l++) {
@@ -1390,7 +1462,7 @@ int t5h_layer_forward(t5h_model* m, int32_t layer, const float* x_in, const int3
   if ((rc = validate_cu(m, cu, B, T))) return rc;
   if (T == 0) return T5H_OK;
   if (!x_in || !x_out) return fail(T5H_ERR_INVALID, "NULL buffer");
-  if ((rc = ensure_workspace(m, T, B, (T + 63) / 64 + B))) return rc;
+  if ((rc = ensure_workspace(m, T, B, attn_work_cap(m, T, B)))) return rc;
   int nwork = 0;
   if ((rc = upload_batch(m, cu, B, nwork))) return rc;
   const size_t bytes = (size_t)T * m->cfg.d_model * 4;
@@ -1407,7 +1479,7 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   if (T <= 0 || !x || !y) return fail(T5H_ERR_INVALID, "bad FFN block arguments");
   if (mode != 0 && mode != 1) return fail(T5H_ERR_INVALID, "mode must be 0 or 1");
   if (!m->cfg.feed_forward_gated) return fail(T5H_ERR_INVALID, "model FFN is not gated");
-  if ((rc = ensure_workspace(m, T, 1, (T + 63) / 64 + 1))) return rc;
+  if ((rc = ensure_workspace(m, T, 1, attn_work_cap(m, T, 1)))) return rc;
   const t5h_config& c = m->cfg;
   const Layer& Ly = m->layers[layer];
   const size_t bytes = (size_t)T * c.d_model * 4;
