@@ -88,6 +88,9 @@ __host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
   return s;
 }
 
+// Queries per attention workgroup (one work list item): 4 waves x 16.
+constexpr int ATTN_QT = 64;
+
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]
   _Float16* out;        // [T][H*dkv] in operand order (tiled_index)

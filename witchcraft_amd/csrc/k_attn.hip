@@ -23,7 +23,7 @@
 
 namespace {
 
-constexpr int QT = 64;   // queries per workgroup
+constexpr int QT = ATTN_QT;  // queries per workgroup
 constexpr int KT = 64;   // keys per tile
 constexpr int DK = 64;   // head dim (d_kv)
 constexpr float LOG2E = 1.4426950408889634f;

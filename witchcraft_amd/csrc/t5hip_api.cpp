@@ -341,7 +341,7 @@ int add_f32_vector(HostArena& ha, const t5h::GgufFile& g, const std::string& nam
 }
 
 // Rows every workspace buffer holds for T tokens: GEMM tiles read A rows up to
-// roundup(T, 512); attention reads up to T + 63.
+// roundup(T, 512); attention reads up to T + ATTN_QT - 1.
 int workspace_tpad(int T) { return (T + 511) / 512 * 512 + 128; }
 
 // Lays the workspace of tpad rows and capW attention work items out from `base` (nullptr:
@@ -602,12 +602,12 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
 // and each goes to the XCD with the least work (query tiles x key tiles) among those whose
 // list stays within ceil(items / 8) + the longest group, which bounds the padding: the lists
 // are padded to the longest one with empty items (length 0), which exit at once.
-int attn_tiles(int L) { return (L + 63) / 64; }
+int attn_tiles(int L) { return (L + ATTN_QT - 1) / ATTN_QT; }
 
 // Upper bound of the work list length (items incl. padding) for T tokens in B sequences of at
 // most max_len tokens.
 int attn_work_cap(const t5h_model* m, int T, int B) {
-  return m->cfg.num_heads * ((T + 63) / 64 + B) + 8 * (attn_tiles(m->cfg.max_seq_len) + 1);
+  return m->cfg.num_heads * ((T + ATTN_QT - 1) / ATTN_QT + B) + 8 * (attn_tiles(m->cfg.max_seq_len) + 1);
 }
 
 // Calls emit(group) for every (sequence, head) in `order`; returns the slots per XCD.
@@ -679,7 +679,7 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   if (!s.done) HIP_OK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
   int4* hw = (int4*)s.host;
   for (const AttnGroup& g : m->groups)
-    for (int q = 0; q < attn_tiles(g.len); q++) hw[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * 64, g.head);
+    for (int q = 0; q < attn_tiles(g.len); q++) hw[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * ATTN_QT, g.head);
   for (int x = 0; x < 8; x++)
     for (int q = xlen[x]; q < slots; q++) hw[(size_t)q * 8 + x] = make_int4(0, 0, 0, 0);
   m->attn_flops = 0;
@@ -1186,9 +1186,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   if (rb->type != t5h::GGML_F32 || rb->shape.size() != 2 ||
       (int)rb->rows() != cfg->relative_attention_num_buckets || (int)rb->cols() != H)
     return fail(T5H_ERR_FORMAT, "tensor " + rb_name + ": expected F32 [num_buckets, num_heads]");
-  // The attention kernel reads distances up to the padded sequence length + 1 (64-key
-  // tiles), so the LUT covers |j - i| <= roundup(max_seq_len, 64) + 64.
-  const int lutw = (cfg->max_seq_len + 63) / 64 * 64 + 64, span = 2 * lutw + 1;
+  // The attention kernel stages the bias of distances k0 - q0 - (ATTN_QT - 1) .. k0 - q0 + 64
+  // (64-key tiles, ATTN_QT-query workgroups), so the LUT covers |j - i| <= roundup(max_seq_len,
+  // 64) + ATTN_QT.
+  const int lutw = (cfg->max_seq_len + 63) / 64 * 64 + ATTN_QT, span = 2 * lutw + 1;
   const size_t lut_off = ha.add(nullptr, (size_t)H * span * 4);
   {
     float* lut = reinterpret_cast<float*>(ha.bytes.data() + lut_off);
