@@ -30,7 +30,10 @@
 
 namespace {
 
-constexpr int BK = 64, LDSK = BK + 8;  // +16 B row pad
+// Weight stage rows of 64 halves, unpadded; 16-byte chunk c of row r is stored at c ^ (r & 7),
+// so the math waves' fragment reads (16 rows x 4 chunks per instruction) hit every bank once.
+constexpr int BK = 64, LDSK = BK;
+__device__ __forceinline__ int bswz(int r, int c) { return r * LDSK + ((((c >> 3) ^ r) & 7) << 3) + (c & 7); }
 
 // B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns
 // n0.., rows [BN/2, BN) the same W1 columns, so a math wave's N blocks nb < NB/2 (gate)
@@ -104,22 +107,21 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
     const int c = ((kt * BK) % QK_K) / 64;
     float s0, o0, s1, o1;
     chunk_scales(br.hd, c, s0, o0, s1, o1);
-    _Float16* row = Bs + r * LDSK;
 #pragma unroll
     for (int w = 0; w < R::NQ; w += 2) {
       h4 lo0, hi0, lo1, hi1;
       deq4(br.q[w], s0, o0, s1, o1, lo0, hi0);
       deq4(br.q[w + 1], s0, o0, s1, o1, lo1, hi1);
-      *reinterpret_cast<h8*>(row + part * R::BPT + 4 * w) =
+      *reinterpret_cast<h8*>(Bs + bswz(r, part * R::BPT + 4 * w)) =
           h8{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
-      *reinterpret_cast<h8*>(row + 32 + part * R::BPT + 4 * w) =
+      *reinterpret_cast<h8*>(Bs + bswz(r, 32 + part * R::BPT + 4 * w)) =
           h8{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
     }
   } else {
 #pragma unroll
     for (int i = 0; i < R::F16_LOADS; i++) {
       const int idx = i * NP + pt, r = idx >> 3, c8 = (idx & 7) * 8;
-      *reinterpret_cast<u4v*>(Bs + r * LDSK + c8) = br.f[i];
+      *reinterpret_cast<u4v*>(Bs + bswz(r, c8)) = br.f[i];
     }
   }
 }
@@ -349,7 +351,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
   __syncthreads();
 
   // nkt % S == 0 (K % 256 == 0); as in the producers, loads past the end are clamped
-  const _Float16* bbase = &Bs[0][lr * LDSK + 8 * lg];
+  // fragment (nb, s) of this lane: row 16 nb + lr, columns 32 s + 8 lg .. +7 (row & 7 = lr & 7)
+  const _Float16* bbase0 = &Bs[0][bswz(lr, 8 * lg)];
+  const _Float16* bbase1 = &Bs[0][bswz(lr, 32 + 8 * lg)];
   for (int kt0 = 0; kt0 < nkt; kt0 += S) {
 #pragma unroll
     for (int u = 0; u < S; u++) {
@@ -357,7 +361,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
       {
         LOAD_A((u + S - 1) % S, min(kt + S - 1, nkt - 1));
         __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this step's MFMAs
-        const _Float16* bsrc = bbase + (kt & 1) * (BN * LDSK);
+        const _Float16* bsrc0 = bbase0 + (kt & 1) * (BN * LDSK);
+        const _Float16* bsrc1 = bbase1 + (kt & 1) * (BN * LDSK);
         // Weight fragments j = s * NB + nb in order, each read FD fragments ahead of its MFMAs
         // so that the LDS latency hides behind the MFMAs of the fragments before it; the
         // scheduling barriers keep the compiler from regrouping the reads.
@@ -365,12 +370,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
         h8 wf[FD + 1];
 #pragma unroll
         for (int j = 0; j < FD; j++)
-          wf[j] = *reinterpret_cast<const h8*>(bsrc + (j % NB) * 16 * LDSK + 32 * (j / NB));
+          wf[j] = *reinterpret_cast<const h8*>((j / NB ? bsrc1 : bsrc0) + (j % NB) * 16 * LDSK);
 #pragma unroll
         for (int j = 0; j < NF; j++) {
           if (j + FD < NF)
             wf[(j + FD) % (FD + 1)] =
-                *reinterpret_cast<const h8*>(bsrc + ((j + FD) % NB) * 16 * LDSK + 32 * ((j + FD) / NB));
+                *reinterpret_cast<const h8*>(((j + FD) / NB ? bsrc1 : bsrc0) + ((j + FD) % NB) * 16 * LDSK);
           const int s = j / NB, nb = j % NB;
 #pragma unroll
           for (int mb = 0; mb < MB; mb++)
