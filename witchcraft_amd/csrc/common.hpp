@@ -102,6 +102,13 @@ struct AttnArgs {
 
 // Device-side helpers ---------------------------------------------------------
 
+// LDS tiles of f16 with 64-half rows, unpadded, where 16-byte chunk c of row r is stored at
+// chunk c ^ (r & 7): a read of 16 rows x one chunk (ds_read_b128) and a transposed read of 16
+// rows x 32 bytes (ds_read_b64_tr_b16) each hit every bank once (measured with probe kernels).
+__device__ __forceinline__ int swz64(int row, int col) {
+  return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   _Float16 h;
   uint16_t b = (uint16_t)bits16;

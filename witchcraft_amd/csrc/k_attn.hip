@@ -30,12 +30,9 @@ constexpr float LOG2E = 1.4426950408889634f;
 
 typedef short s4v __attribute__((ext_vector_type(4)));
 
-// LDS tiles are 64 keys x 64 dims of f16, 128 B per row, unpadded, with the eight 16-byte
-// chunks of row r stored in the order chunk ^ (r & 7).  Both operand reads (K: 16 rows x one
-// 16-byte chunk per instruction; V: 16 rows x 32 bytes, transposed) then hit every bank once.
-__device__ __forceinline__ int swz(int row, int col) {
-  return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
-}
+// LDS tiles are 64 keys x 64 dims of f16 in the swz64 layout (128 B rows, XOR-swizzled
+// 16-byte chunks): the K operand reads and the transposed V reads are conflict-free.
+__device__ __forceinline__ int swz(int row, int col) { return swz64(row, col); }
 
 // Global -> LDS copy of one 64-row tile by this wave's 16 rows: LDS slot l of an instruction
 // (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ (row % 8), so

@@ -30,10 +30,10 @@
 
 namespace {
 
-// Weight stage rows of 64 halves, unpadded; 16-byte chunk c of row r is stored at c ^ (r & 7),
-// so the math waves' fragment reads (16 rows x 4 chunks per instruction) hit every bank once.
+// Weight stage rows of 64 halves in the swz64 layout, so the math waves' fragment reads (16 rows
+// x 4 chunks per instruction) hit every bank once.
 constexpr int BK = 64, LDSK = BK;
-__device__ __forceinline__ int bswz(int r, int c) { return r * LDSK + ((((c >> 3) ^ r) & 7) << 3) + (c & 7); }
+__device__ __forceinline__ int bswz(int r, int c) { return swz64(r, c); }
 
 // B-tile row r -> (weight matrix, output column).  Gated: rows [0, BN/2) are W0 columns
 // n0.., rows [BN/2, BN) the same W1 columns, so a math wave's N blocks nb < NB/2 (gate)
