@@ -64,6 +64,7 @@ SIGNATURES = {
     "t5h_q8k_quantize": (C.c_int, [C.c_int32, _f32p, C.c_int32, C.c_int32, _u8p]),
     "t5h_q4k_q8k_matmul": (C.c_int, [C.c_int32, _u8p, C.c_int32, _u8p, C.c_int32, C.c_int32, _f32p]),
     "t5h_q4k_dequant_f32": (C.c_int, [_u8p, C.c_size_t, _f32p, C.c_int]),
+    "t5h_attention_work": (C.c_int, [_i32p, C.c_int32, C.c_int32, _i32p, C.c_int32, C.POINTER(C.c_int32)]),
     "t5h_matmul_t": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _f32p]),
     "t5h_matmul_argmax": (C.c_int, [C.c_int32, _f32p, C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, _u32p]),
     "t5h_matmul_t_device": (C.c_int, [_vp, C.c_int32, _vp, C.c_int32, C.c_int32, C.c_int32, _vp, _vp]),

@@ -183,7 +183,6 @@ struct t5h_model {
   const float* rel_lut = nullptr;  // [H][2*lutw+1], bias of distance j - i at lutw + j - i
   int lutw = 0, lut_sat = 0;  // lut_sat: |j - i| from which the bias is the LUT's end value
   std::vector<int> order;  // host scratch: sequence order of the attention work list
-  std::vector<AttnGroup> groups;  // host scratch: the attention work plan
   std::vector<int32_t> last_cu;  // cu_seqlens of the batch whose cu / work list are on the device
   int last_B = -1, last_nwork = 0;
   double attn_flops = 0;   // QK^T + PV flops of one attention launch on the current batch, true tokens
@@ -606,15 +605,14 @@ int attn_tiles(int L) { return (L + ATTN_QT - 1) / ATTN_QT; }
 
 // Upper bound of the work list length (items incl. padding) for T tokens in B sequences of at
 // most max_len tokens.
-int attn_work_cap(const t5h_model* m, int T, int B) {
-  return m->cfg.num_heads * ((T + ATTN_QT - 1) / ATTN_QT + B) + 8 * (attn_tiles(m->cfg.max_seq_len) + 1);
+int attn_work_cap(int heads, int max_seq_len, int T, int B) {
+  return heads * ((T + ATTN_QT - 1) / ATTN_QT + B) + 8 * (attn_tiles(max_seq_len) + 1);
 }
+int attn_work_cap(const t5h_model* m, int T, int B) { return attn_work_cap(m->cfg.num_heads, m->cfg.max_seq_len, T, B); }
 
 // Calls emit(group) for every (sequence, head) in `order`; returns the slots per XCD.
 template <class Emit>
-int plan_attention(const t5h_model* m, const int32_t* cu, const std::vector<int>& order, int (&xlen)[8],
-                   Emit&& emit) {
-  const int H = m->cfg.num_heads;
+int plan_attention(int H, const int32_t* cu, const std::vector<int>& order, int (&xlen)[8], Emit&& emit) {
   long long items = 0, load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   int maxq = 0;
   for (int b : order) {
@@ -640,12 +638,24 @@ int plan_attention(const t5h_model* m, const int32_t* cu, const std::vector<int>
   return slots;
 }
 
-// Longest sequences first into m->order (m->order is the handle's host scratch).
-void order_by_length(t5h_model* m, const int32_t* cu, int B) {
-  m->order.resize(B);
-  for (int b = 0; b < B; b++) m->order[b] = b;
-  std::stable_sort(m->order.begin(), m->order.end(),
-                   [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+// Longest sequences first (order is host scratch, reused across calls).
+void order_by_length(std::vector<int>& order, const int32_t* cu, int B) {
+  order.resize(B);
+  for (int b = 0; b < B; b++) order[b] = b;
+  std::stable_sort(order.begin(), order.end(), [cu](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+}
+
+// The work list upload_batch writes: item (slot q of XCD x) at index 8 q + x.
+int write_attention_work(int H, const int32_t* cu, const std::vector<int>& order, int4* out, size_t cap) {
+  int xlen[8];
+  const int slots = plan_attention(H, cu, order, xlen, [](const AttnGroup&) {});
+  if ((size_t)8 * slots > cap) return -1;
+  plan_attention(H, cu, order, xlen, [&](const AttnGroup& g) {
+    for (int q = 0; q < attn_tiles(g.len); q++) out[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * ATTN_QT, g.head);
+  });
+  for (int x = 0; x < 8; x++)
+    for (int q = xlen[x]; q < slots; q++) out[(size_t)q * 8 + x] = make_int4(0, 0, 0, 0);
+  return 8 * slots;
 }
 
 // Uploads the attention work list through a pinned staging slot: one (start, length, first
@@ -658,11 +668,9 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
     return T5H_OK;
   }
   m->last_B = -1;
-  order_by_length(m, cu, B);
+  order_by_length(m->order, cu, B);
   int xlen[8];
-  m->groups.clear();
-  const int slots = plan_attention(m, cu, m->order, xlen, [m](const AttnGroup& g) { m->groups.push_back(g); });
-  nwork = 8 * slots;
+  nwork = 8 * plan_attention(m->cfg.num_heads, cu, m->order, xlen, [](const AttnGroup&) {});
   if (nwork > m->cap_work) return fail(T5H_ERR_INVALID, "internal: attention work list exceeds its capacity");
   StagingSlot& s = m->slots[m->next_slot];
   m->next_slot = (m->next_slot + 1) % 4;
@@ -678,10 +686,8 @@ int upload_batch(t5h_model* m, const int32_t* cu, int B, int& nwork) {
   }
   if (!s.done) HIP_OK(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
   int4* hw = (int4*)s.host;
-  for (const AttnGroup& g : m->groups)
-    for (int q = 0; q < attn_tiles(g.len); q++) hw[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * ATTN_QT, g.head);
-  for (int x = 0; x < 8; x++)
-    for (int q = xlen[x]; q < slots; q++) hw[(size_t)q * 8 + x] = make_int4(0, 0, 0, 0);
+  if (write_attention_work(m->cfg.num_heads, cu, m->order, hw, (size_t)nwork) != nwork)
+    return fail(T5H_ERR_INVALID, "internal: attention work plan changed between passes");
   m->attn_flops = 0;
   for (int b = 0; b < B; b++)
     m->attn_flops += 4.0 * (double)(cu[b + 1] - cu[b]) * (cu[b + 1] - cu[b]) * m->cfg.d_kv * m->cfg.num_heads;
@@ -932,9 +938,9 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
   if (T == 0) return T5H_OK;
   if (!d_ids || !d_out) return fail(T5H_ERR_INVALID, "d_ids/d_out must not be NULL");
   if (!m->scratch) return fail(T5H_ERR_HIP, "no-alloc scratch array is not mapped on this device");
-  order_by_length(m, cu, B);
+  order_by_length(m->order, cu, B);
   int xlen[8];
-  const int nwork = 8 * plan_attention(m, cu, m->order, xlen, [](const AttnGroup&) {});
+  const int nwork = 8 * plan_attention(m->cfg.num_heads, cu, m->order, xlen, [](const AttnGroup&) {});
   const int tpad = workspace_tpad(T);
   Workspace w;
   const size_t need = carve_workspace(m, tpad, nwork, nullptr, w);
@@ -958,7 +964,8 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
       ch.n = 0;
     }
   };
-  plan_attention(m, cu, m->order, xlen, [&](const AttnGroup& g) { add(g.start, g.len, g.head, g.slot0 * 8 + g.xcd); });
+  plan_attention(m->cfg.num_heads, cu, m->order, xlen,
+                 [&](const AttnGroup& g) { add(g.start, g.len, g.head, g.slot0 * 8 + g.xcd); });
   for (int x = 0; x < 8; x++)
     if (xlen[x] < nwork / 8) add(nwork / 8 - xlen[x], 0, 0, xlen[x] * 8 + x);
   if (herr == hipSuccess) herr = t5k::launch_work_list(ch, w.work, m->stream);
@@ -1520,6 +1527,19 @@ int t5h_set_numerics(t5h_model* m, int32_t mode) {
     return fail(T5H_ERR_INVALID, "hybrid numerics: Q8_K rows do not fit the attention output buffer");
   HIP_OK(hipStreamSynchronize(m->stream));
   m->numerics = mode;
+  return T5H_OK;
+}
+
+int t5h_attention_work(const int32_t* cu, int32_t B, int32_t heads, int32_t* items, int32_t cap, int32_t* n_items) {
+  if (!cu || !items || !n_items || B < 0 || heads < 1 || cap < 0) return fail(T5H_ERR_INVALID, "bad arguments");
+  if (cu[0] != 0) return fail(T5H_ERR_INVALID, "cu_seqlens[0] must be 0");
+  for (int b = 0; b < B; b++)
+    if (cu[b + 1] < cu[b]) return fail(T5H_ERR_INVALID, "cu_seqlens must be non-decreasing");
+  std::vector<int> order;
+  order_by_length(order, cu, B);
+  const int n = write_attention_work(heads, cu, order, reinterpret_cast<int4*>(items), (size_t)cap);
+  if (n < 0) return fail(T5H_ERR_INVALID, "attention work list longer than cap");
+  *n_items = n;
   return T5H_OK;
 }
 

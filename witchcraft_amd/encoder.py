@@ -218,6 +218,19 @@ class T5ModelBuilder:
         return T5EncoderModel(model_bytes, self.config, dev)
 
 
+def attention_work(cu_seqlens: np.ndarray, heads: int) -> np.ndarray:
+    """The attention work list the encoder uploads for a batch: [n, 4] int32 items (sequence
+    start, length, first query, head), one per 64-query workgroup, length 0 for the padding of
+    the 8 per-XCD lists; item i runs on XCD i % 8.  Host only."""
+    cu = np.ascontiguousarray(cu_seqlens, np.int32).reshape(-1)
+    B = cu.size - 1
+    cap = heads * (int(cu[-1]) // 64 + 2 * B + 8) + 8 * 64 + 64 if B > 0 else 64
+    items = np.zeros(cap * 4, np.int32)
+    n = C.c_int32(0)
+    check(lib.t5h_attention_work(cu, B, heads, items, cap, C.byref(n)))
+    return items[: 4 * n.value].reshape(-1, 4)
+
+
 def q8k_quantize(x: np.ndarray, hip_device: int = 0) -> np.ndarray:
     """BlockQ8K::from_float on the GPU (src/fused_matmul.rs:36-41): f32 [rows, cols]
     (cols % 256 == 0) -> uint8 [rows, cols / 256 * 292]."""
