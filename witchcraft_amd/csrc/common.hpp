@@ -65,6 +65,8 @@ struct GemmArgs {
   float* rec_next;
   _Float16* nx;
   const float* ngamma;
+  // GEMV only: compute units of the device, for the grid shape (0: 256).
+  int cus;
 };
 
 // Largest row length (d_model) whose sums of squares fit a norm record (15 slots of 64).

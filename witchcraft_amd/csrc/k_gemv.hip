@@ -6,10 +6,10 @@
 // (reference: the query-side forward of T5EncoderModel, src/quantized_t5.rs:698-701, one
 // [1, L] sequence at a time, L ~ 32).
 //
-//  * One workgroup owns 16 weight rows (one MFMA A operand) and every token (MT blocks of
-//    16, M <= 64); up to 16 wave64s split K into equal ranges of one or two 64-wide chunks
-//    (K = 768: 12 waves; K = 2048: 16 waves), so a launch has N/16 workgroups and every
-//    weight byte is read by exactly one lane.
+//  * One workgroup owns 16 weight rows (one MFMA A operand) and MT blocks of 16 tokens (one, or
+//    two where one would overflow the CUs, launch_wf); up to 16 wave64s split K into equal
+//    ranges of one or two 64-wide chunks (K = 768: 12 waves; K = 2048: 16 waves), so every
+//    weight byte of a token slice is read by exactly one lane.
 //  * Each wave issues the raw loads of its chunks (Q4_K header + 8 nibble bytes per lane,
 //    plus the activation operands) before unpacking any of them: one memory round trip.
 //  * The partial accumulators meet in LDS and are summed in wave order (results do not
@@ -352,11 +352,18 @@ hipError_t launch_mt(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// One workgroup per 16 weight rows and 16 tokens: every workgroup streams the activations of
-// its own 16 tokens only, which is what bounds these launches (each CU receives activation
-// bytes at a fixed rate), while the weight rows are re-read per token block from L2.
+// Token blocks per workgroup.  Each workgroup streams the activations of its own tokens, which
+// is what bounds these launches (each CU receives activation bytes at a fixed rate), while the
+// weight rows are re-read per token block from L2.  So one 16-token block per workgroup, unless
+// that overflows the CUs into a second, mostly empty round of workgroups: then all tokens of a
+// 32-token block pair (QKV, N = 2304 at 32 tokens: 288 -> 144 workgroups, 5.1 -> 4.2 us).  Both
+// give the same bits: an output's K order is fixed by the waves' K split alone.  (Half blocks of
+// 8 tokens for the N = 768 launches, 192 workgroups, measured slower: wo 5.4 -> 6.1 us.)
 template <int EPI, int WF, bool NORM>
 hipError_t launch_wf(const GemmArgs& a, hipStream_t s) {
+  const int cus = a.cus > 0 ? a.cus : 256, cols = a.N / 16;
+  const int b16 = (a.M + 15) / 16, b32 = (a.M + 31) / 32;
+  if (cols * b16 > cus && b32 < b16) return launch_mt<EPI, WF, 2, NORM>(a, s);
   return launch_mt<EPI, WF, 1, NORM>(a, s);
 }
 

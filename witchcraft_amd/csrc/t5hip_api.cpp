@@ -548,6 +548,7 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   a.heads = m->cfg.num_heads;
   a.dkv = m->cfg.d_kv;
   a.tpad = m->w.tpad;
+  a.cus = m->cus;
   const double mats = W1 ? 2.0 : 1.0;
   const double flops = 2.0 * M * W.N * W.K * mats;
   const double out_bytes = (epi == EPI_F32 || epi == EPI_RESID ? 4.0 : 2.0) * M * W.N *
