@@ -152,7 +152,8 @@ int t5h_quantize_q4k(const float* x, int64_t n_values, uint8_t* out, int32_t thr
  * Host buffers. */
 int t5h_q8k_quantize(int32_t hip_device, const float* x, int32_t rows, int32_t cols, uint8_t* blocks);
 /* out[T][N] = vec_dot(w row n, x8 row t) for Q4_K rows w[N][K] and Q8_K rows x8[T][K]
- * (BlockQ4K::vec_dot, src/fused_matmul.rs:55; N % 4 == 0).  Host buffers. */
+ * (BlockQ4K::vec_dot, src/fused_matmul.rs:55), through the same matrix-core kernel as the hybrid
+ * numerics of the forward (N % 64 == 0, K % 256 == 0, K <= 1024).  Host buffers. */
 int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const uint8_t* x8, int32_t T,
                        int32_t K, float* out);
 

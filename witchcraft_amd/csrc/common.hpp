@@ -67,6 +67,12 @@ struct GemmArgs {
   const float* ngamma;
   // GEMV only: compute units of the device, for the grid shape (0: 256).
   int cus;
+  // Hybrid numerics (launch_gemm_hybrid): A holds the Q8_K integers q8 of every token as f16
+  // (exact), d8 [Mpad][K/256] their block scales, bsop the blocks' 16 bsums as the B operand of
+  // one 16x16x32 MFMA per (16-token row block, K block) -- 1 KiB blocks [Mpad/16][K/256], lane l
+  // = (token l % 16, K slots 8 (l / 16) .. +7): bsum 8 (l / 16) + e for l < 32, zero for l >= 32.
+  const float* d8;
+  const _Float16* bsop;
 };
 
 // Largest row length (d_model) whose sums of squares fit a norm record (15 slots of 64).
@@ -147,6 +153,20 @@ __device__ __forceinline__ float gelu_tanh_dev(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
+// candle's Pade tanh (src/fused_matmul.rs:128-133) and the gelu of the hybrid-dequant gated FFN
+// (:168-170), in f32 with no contraction, as the reference's scalar code rounds it.
+__device__ __forceinline__ float fast_tanh_pade(float x) {
+#pragma clang fp contract(off)
+  x = x < -4.97f ? -4.97f : (x > 4.97f ? 4.97f : x);
+  const float x2 = x * x;
+  return x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2))) /
+         (135135.0f + x2 * (62370.0f + x2 * (3150.0f + 28.0f * x2)));
+}
+__device__ __forceinline__ float gelu_pade(float g) {
+#pragma clang fp contract(off)
+  return 0.5f * g * (1.0f + fast_tanh_pade(0.7978845608f * g * (1.0f + 0.044715f * g * g)));
+}
+
 // Host-side launchers (defined in the .hip files) --------------------------------
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
@@ -197,12 +217,18 @@ hipError_t launch_embed_batch(const float* win, const int4* docs, const int* tok
 // Blocks of tokens the embed kernels use for N tokens (block_counts / block_offsets need one more).
 int embed_batch_blocks(int N);
 // Hybrid-dequant numerics (k_q8k.hip): f32 rows [T][D] (T5LayerNorm with gamma first, unless
-// gamma is null) -> GGML Q8_K blocks [T][D/256]; then Q4_K weights [N][K] x Q8_K rows by
-// integer dot products: f32 out [T][ldo] (W1 null) or gelu_pade(W0 row) * (W1 row) as the f16
-// operand [T][N] of the next GEMM (operand order).
+// gamma is null) quantized to GGML Q8_K; the result as Q8_K blocks [T][D/256] (out, may be
+// null) and/or as the operands of launch_gemm_hybrid (xq, d8, bsop as GemmArgs describes them;
+// xq null: not written).  launch_q8k_operands converts Q8_K blocks to those operands.
 int q8k_bytes_per_row(int D);
 hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, int T, int D, uint8_t* out,
+                               hipStream_t s, _Float16* xq = nullptr, float* d8 = nullptr, _Float16* bsop = nullptr);
+hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, _Float16* xq, float* d8, _Float16* bsop,
                                hipStream_t s);
-hipError_t launch_q4k_q8k(const uint8_t* W0, const uint8_t* W1, const uint8_t* X8, int T, int N, int K, float* outf,
-                          int ldo, _Float16* outh, hipStream_t s);
+// Q4_K weights x Q8_K activations on the matrix cores (k_gemm.hip): per K block of 256, f16(sc * q4)
+// against f16(q8) sums the block's integers in the f32 accumulator (exact below 2^24); the block
+// then adds d4 d8 * sum - dmin4 d8 * (mins . bsums) in f32.  epi: EPI_GATED (gelu_pade(W0) *
+// W1 into the f16 operand, operand order) or EPI_F32.  Q4_K weights, bn = 64, K <= 1024.
+GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus);
+hipError_t launch_gemm_hybrid(int epi, const GemmPlan& plan, const GemmArgs& a, hipStream_t s);
 }  // namespace t5k

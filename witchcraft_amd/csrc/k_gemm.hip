@@ -126,6 +126,60 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
   }
 }
 
+// Hybrid numerics (launch_gemm_hybrid): the stage holds f16(sc * q) -- the sub-block scale times
+// the nibble, an integer <= 945, exact -- instead of the dequantized value (deq4 with the scale
+// 2^9 sc and no min: (q 2^-9)(sc 2^9) = sc q exactly).  At the first K step of a 256-wide block
+// the row's first producer thread also writes the block's d and dmin (Md) and its eight 6-bit
+// mins as the A operand of the min-term MFMA (Mm: m0 m0 m1 m1 .. m7 m7, one per bsum).
+template <int NP, int BN>
+__device__ __forceinline__ void store_b_hybrid(const BRaw<WF_Q4K, NP, BN>& br, _Float16* Bs, float2* Md, h8* Mm,
+                                               int kt, int pt) {
+  using R = BRaw<WF_Q4K, NP, BN>;
+  const int r = pt / R::TPR, part = pt % R::TPR;
+  const int c = ((kt * BK) % QK_K) / 64;
+  const uint4 hd = br.hd;
+  // get_scale_min_k4 on the 12 scale bytes (header words y, z, w); sub-blocks 2c, 2c + 1
+  auto byte = [&](int i) -> int {
+    const uint32_t w = i < 4 ? hd.y : (i < 8 ? hd.z : hd.w);
+    return (int)((w >> (8 * (i & 3))) & 0xff);
+  };
+  auto scale_min = [&](int j, int& sc, int& m) {
+    if (j < 4) {
+      sc = byte(j) & 63;
+      m = byte(j + 4) & 63;
+    } else {
+      sc = (byte(j + 4) & 15) | ((byte(j - 4) >> 6) << 4);
+      m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+  };
+  int sc0, m0, sc1, m1;
+  scale_min(2 * c, sc0, m0);
+  scale_min(2 * c + 1, sc1, m1);
+  const float s0 = 512.0f * (float)sc0, s1 = 512.0f * (float)sc1;
+#pragma unroll
+  for (int w = 0; w < R::NQ; w += 2) {
+    h4 lo0, hi0, lo1, hi1;
+    deq4(br.q[w], s0, 0.f, s1, 0.f, lo0, hi0);
+    deq4(br.q[w + 1], s0, 0.f, s1, 0.f, lo1, hi1);
+    *reinterpret_cast<h8*>(Bs + bswz(r, part * R::BPT + 4 * w)) =
+        h8{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
+    *reinterpret_cast<h8*>(Bs + bswz(r, 32 + part * R::BPT + 4 * w)) =
+        h8{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+  }
+  if (c == 0 && part == 0) {
+    Md[r] = make_float2(f16_bits_to_f32(hd.x & 0xffff), f16_bits_to_f32(hd.x >> 16));
+    _Float16 mh[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int sc, m;
+      scale_min(j, sc, m);
+      mh[j] = (_Float16)m;
+    }
+    Mm[2 * r] = h8{mh[0], mh[0], mh[1], mh[1], mh[2], mh[2], mh[3], mh[3]};
+    Mm[2 * r + 1] = h8{mh[4], mh[4], mh[5], mh[5], mh[6], mh[6], mh[7], mh[7]};
+  }
+}
+
 // QKV epilogue through LDS (d_kv = 64).  The accumulators give each lane 4 columns of one
 // token, so direct stores into the head-major [3][H][tpad][64] layout write 16 x 32-byte
 // pieces per instruction.  Instead each 16-token block is staged in this wave's LDS region
@@ -275,11 +329,127 @@ __device__ __forceinline__ float norm_factor(const GemmArgs& p, int mrow0, int n
   return inv / d.w;
 }
 
+// Math waves of a hybrid-numerics tile (launch_gemm_hybrid).  The stage holds f16(sc * q4) and the
+// A operand the Q8_K integers q8, so the MFMAs sum sc q4 q8 over a 256-wide K block exactly in the
+// f32 accumulator as long as partial sums stay below 2^24 (the sums' bound is 256 * 945 * 128;
+// quantized rows come nowhere near it, and beyond it the f32 sum is still within one unit in the
+// last place of the exact integer).  After its four K steps the block is folded into the output:
+//   out += (d4 d8) * sum  -  (dmin4 d8) * (mins . bsums),
+// the min term from one more MFMA of the row's mins (Mm) against the tokens' bsums (bsop).  This is
+// vec_dot's d * d8 * sum_j sc_j (q4 . q8)_j - dmin * d8 * sum_j m_j (bsum_2j + bsum_2j+1) per block
+// (src/fused_matmul.rs:36-41,147-172), with the f32 combination in this order.
+template <int EPI, int MW, int BN, int S, int MB>
+__device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK],
+                                            const float2 (*Md)[BN], const h8 (*Mm)[2 * BN]) {
+  constexpr int NB = BN / 16;
+  static_assert(S == 2, "the hybrid loop unrolls a K block as two A stages");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+  const int nkt = p.K / BK, nblk = p.K / QK_K;
+  const int mrow0 = m0 + wave * 16 * MB;
+  const size_t kblk = p.K / 32;
+  const _Float16* ablk[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) ablk[mb] = p.A + ((size_t)(mrow0 / 16 + mb) * kblk) * 512 + lane * 8;
+
+  f4 acc[MB][NB], out[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) out[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  uint4 a[S][MB][2];
+#define LOAD_A(st, kt)                                                                      \
+  _Pragma("unroll") for (int mb = 0; mb < MB; mb++) {                                        \
+    a[st][mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);     \
+    a[st][mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512); \
+  }
+  LOAD_A(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+
+  const _Float16* bbase0 = &Bs[0][bswz(lr, 8 * lg)];
+  const _Float16* bbase1 = &Bs[0][bswz(lr, 32 + 8 * lg)];
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < nblk; b++) {
+    // the block's d8 and bsum operand of every row block, requested before its MFMAs
+    float d8v[MB];
+    uint4 bsf[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      d8v[mb] = p.d8[(size_t)(mrow0 + 16 * mb + lr) * nblk + b];
+      bsf[mb] = *reinterpret_cast<const uint4*>(p.bsop + ((size_t)(mrow0 / 16 + mb) * nblk + b) * 512 + lane * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int kt = 4 * b + u;
+      LOAD_A((u + 1) % S, min(kt + 1, nkt - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      const _Float16* bsrc0 = bbase0 + (kt & 1) * (BN * LDSK);
+      const _Float16* bsrc1 = bbase1 + (kt & 1) * (BN * LDSK);
+      constexpr int NF = 2 * NB, FD = 2;
+      h8 wf[FD + 1];
+#pragma unroll
+      for (int j = 0; j < FD; j++) wf[j] = *reinterpret_cast<const h8*>((j / NB ? bsrc1 : bsrc0) + (j % NB) * 16 * LDSK);
+#pragma unroll
+      for (int j = 0; j < NF; j++) {
+        if (j + FD < NF)
+          wf[(j + FD) % (FD + 1)] =
+              *reinterpret_cast<const h8*>(((j + FD) / NB ? bsrc1 : bsrc0) + ((j + FD) % NB) * 16 * LDSK);
+        const int sk = j / NB, nb = j % NB;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j % (FD + 1)], __builtin_bit_cast(h8, a[u % S][mb][sk]),
+                                                                (u == 0 && sk == 0) ? zero : acc[mb][nb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __syncthreads();
+    }
+    // fold block b: lane holds rows n0 + 16nb + 4lg + i of token mrow0 + 16mb + lr
+    const int bp = b & 1;
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      const float4 q0 = *reinterpret_cast<const float4*>(&Md[bp][16 * nb + 4 * lg]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&Md[bp][16 * nb + 4 * lg + 2]);
+      const float dd[4] = {q0.x, q0.z, q1.x, q1.z}, dm[4] = {q0.y, q0.w, q1.y, q1.w};
+      const h8 mf = lg < 2 ? Mm[bp][2 * (16 * nb + lr) + lg] : h8{};
+#pragma unroll
+      for (int mb = 0; mb < MB; mb++) {
+        const f4 cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(mf, __builtin_bit_cast(h8, bsf[mb]), zero, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          out[mb][nb][i] = __builtin_fmaf(dd[i] * d8v[mb], acc[mb][nb][i], out[mb][nb][i]);
+          out[mb][nb][i] = __builtin_fmaf(-(dm[i] * d8v[mb]), cm[i], out[mb][nb][i]);
+        }
+      }
+    }
+  }
+#undef LOAD_A
+
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+    const int m = mrow0 + mb * 16 + lr;
+    if (m >= p.M) continue;
+    if constexpr (EPI == EPI_GATED) {
+#pragma unroll
+      for (int nb = 0; nb < NB / 2; nb++) {
+        const f4 g = out[mb][nb], v = out[mb][nb + NB / 2];
+        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
+            h4{(_Float16)(gelu_pade(g[0]) * v[0]), (_Float16)(gelu_pade(g[1]) * v[1]),
+               (_Float16)(gelu_pade(g[2]) * v[2]), (_Float16)(gelu_pade(g[3]) * v[3])};
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) store_quad<EPI_F32>(p, m, n0 + nb * 16 + 4 * lg, out[mb][nb]);
+    }
+  }
+}
+
 // One output tile: tokens [m0, m0 + 16*MB*MW) x weight rows from n0.  MB = 16-row operand
 // blocks per math wave: 4 for full tiles, 1 or 2 for the thin tiles that spread the last,
 // partial round of a launch over every CU (the weight stage per K step is the same).
-template <int EPI, int WF, int MW, int BN, int S, int MB>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK]) {
+template <int EPI, int WF, int MW, int BN, int S, int MB, bool HY = false>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK],
+                                          float2 (*Md)[BN] = nullptr, h8 (*Mm)[2 * BN] = nullptr) {
   constexpr int NP = 64 * MW, NB = BN / 16;
   // S register stages of A (math waves) and PB of raw weights (producers): the loads of a
   // step are issued S-1 (PB-1) steps before it is consumed, covering L2/MALL latency.
@@ -296,8 +466,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
     // steps kt+2 .. kt+PB are in flight.  One barrier per step, as in the math waves.
     const int pt = tid - NP;
     R br[PB];
+    // step kt's weights into stage kt % 2 (hybrid numerics: the block's metadata into kt / 4 % 2)
+    auto store = [&](const R& r, int kt) {
+      if constexpr (HY) store_b_hybrid<NP, BN>(r, Bs[kt & 1], Md[(kt >> 2) & 1], Mm[(kt >> 2) & 1], kt, pt);
+      else store_b<WF, NP, BN>(r, Bs[kt & 1], kt, pt);
+    };
     load_b<EPI, WF, NP, BN>(br[0], p, n0, 0, pt);
-    store_b<WF, NP, BN>(br[0], Bs[0], 0, pt);
+    store(br[0], 0);
 #pragma unroll
     for (int i = 1; i < PB; i++) load_b<EPI, WF, NP, BN>(br[i], p, n0, i, pt);
     __syncthreads();
@@ -307,7 +482,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
 #pragma unroll
       for (int u = 0; u < PB; u++) {
         const int kt = kt0 + u;
-        if (kt + 1 < nkt) store_b<WF, NP, BN>(br[(u + 1) % PB], Bs[(kt + 1) & 1], kt + 1, pt);
+        if (kt + 1 < nkt) store(br[(u + 1) % PB], kt + 1);
         load_b<EPI, WF, NP, BN>(br[u], p, n0, min(kt + PB, nkt - 1), pt);
         __syncthreads();
       }
@@ -316,6 +491,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
   }
 
   // -------------------------------- math waves ---------------------------------
+  if constexpr (HY) {
+    math_hybrid<EPI, MW, BN, S, MB>(p, m0, n0, Bs, Md, Mm);
+    return;
+  }
   const int lr = lane & 15, lg = lane >> 4;
   // operand blocks of this wave's MB row groups: block (rb, kb) at ((rb * K/32) + kb) * 512
   const size_t kblk = p.K / 32;
@@ -430,29 +609,43 @@ struct GemmGrid {
   int tiles_n, main_tiles, main_blocks, m_main, tail_tiles;
 };
 
-template <int EPI, int WF, int MW, int BN, int S, int TMB>
+template <int EPI, int WF, int MW, int BN, int S, int TMB, bool HY = false>
 __global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_kernel(GemmArgs p, GemmGrid g) {
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
+  // hybrid numerics: per-row block metadata (d, dmin; mins as an MFMA operand), two blocks deep
+  __shared__ __attribute__((aligned(16))) float2 Md[HY ? 2 : 1][HY ? BN : 1];
+  __shared__ __attribute__((aligned(16))) h8 Mm[HY ? 2 : 1][HY ? 2 * BN : 1];
   constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN;  // output columns per tile
+  // Full tiles: 4 row blocks per math wave; 2 with hybrid numerics, whose waves hold a second set
+  // of accumulators (the block sums next to the output).
+  constexpr int MBM = HY ? 2 : 4;
   int b = blockIdx.x;
   if (TMB == 0 || b < g.main_blocks) {
     const int tile = (b % 8) * (g.main_blocks / 8) + b / 8;
     if (tile >= g.main_tiles) return;
-    gemm_tile<EPI, WF, MW, BN, S, 4>(p, (tile / g.tiles_n) * 64 * MW, (tile % g.tiles_n) * cols, Bs);
+    if constexpr (HY)
+      gemm_tile<EPI, WF, MW, BN, S, MBM, true>(p, (tile / g.tiles_n) * 16 * MBM * MW, (tile % g.tiles_n) * cols, Bs,
+                                               Md, Mm);
+    else
+      gemm_tile<EPI, WF, MW, BN, S, 4>(p, (tile / g.tiles_n) * 64 * MW, (tile % g.tiles_n) * cols, Bs);
   } else {
     constexpr int MBT = TMB == 0 ? 1 : TMB;
     b -= g.main_blocks;
     const int tile = (b % 8) * (((int)gridDim.x - g.main_blocks) / 8) + b / 8;
     if (tile >= g.tail_tiles) return;
-    gemm_tile<EPI, WF, MW, BN, S, MBT>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
-                                        (tile % g.tiles_n) * cols, Bs);
+    if constexpr (HY)
+      gemm_tile<EPI, WF, MW, BN, S, MBT, true>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
+                                               (tile % g.tiles_n) * cols, Bs, Md, Mm);
+    else
+      gemm_tile<EPI, WF, MW, BN, S, MBT>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
+                                          (tile % g.tiles_n) * cols, Bs);
   }
 }
 
-template <int EPI, int WF, int BN, int S, int MW, int TMB>
+template <int EPI, int WF, int BN, int S, int MW, int TMB, bool HY = false>
 hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
-  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = 64 * MW;
+  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = (HY ? 32 : 64) * MW;
   GemmGrid g;
   g.tiles_n = a.N / cols;
   g.m_main = TMB ? pl.m_main : a.M;
@@ -462,7 +655,7 @@ hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s
   g.tail_tiles = TMB ? (a.M - g.m_main + bmt - 1) / bmt * g.tiles_n : 0;
   const int grid = g.main_blocks + (g.tail_tiles + 7) / 8 * 8;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB>), dim3(grid), dim3(128 * MW), 0, s, a, g);
+  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB, HY>), dim3(grid), dim3(128 * MW), 0, s, a, g);
   return hipGetLastError();
 }
 
@@ -575,6 +768,43 @@ GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override,
       }
     }
   return pl;
+}
+
+// Hybrid plans: full tiles of 32 mw tokens (two row blocks per math wave) x 64 weight rows, or
+// with tail_mb = 1 thin tiles of one row block per math wave for rows [m_main, M).
+GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus) {
+  GemmPlan pl;
+  pl.bn = 64;
+  pl.mw = 4;
+  pl.m_main = M;
+  pl.tail_mb = 0;
+  const int bm = 128, tiles_n = n_rows / 64, full = (M + bm - 1) / bm;
+  double best = list_makespan(full * tiles_n, 0, 1.0, cus);
+  for (int j = full - 1; j >= 0; j--) {
+    const int tail = (M - j * bm + 63) / 64 * tiles_n;
+    const double t = list_makespan(j * tiles_n, tail, 0.6, cus);
+    if (t < best - 1e-9) {
+      best = t;
+      pl.m_main = j * bm;
+      pl.tail_mb = 1;
+    }
+  }
+  return pl;
+}
+
+hipError_t launch_gemm_hybrid(int epi, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (pl.bn != 64 || pl.mw != 4 || a.K % 256 || !a.A || !a.d8 || !a.bsop) return hipErrorInvalidValue;
+  if (pl.tail_mb && (pl.tail_mb != 1 || pl.m_main < 0 || pl.m_main % 128 || pl.m_main >= a.M))
+    return hipErrorInvalidValue;
+  if (epi == EPI_GATED) {
+    if (a.N % 32 || !a.W1) return hipErrorInvalidValue;
+    return pl.tail_mb ? launch_plan<EPI_GATED, WF_Q4K, 64, 2, 4, 1, true>(pl, a, s)
+                      : launch_plan<EPI_GATED, WF_Q4K, 64, 2, 4, 0, true>(pl, a, s);
+  }
+  if (epi != EPI_F32 || a.N % 64) return hipErrorInvalidValue;
+  return pl.tail_mb ? launch_plan<EPI_F32, WF_Q4K, 64, 2, 4, 1, true>(pl, a, s)
+                    : launch_plan<EPI_F32, WF_Q4K, 64, 2, 4, 0, true>(pl, a, s);
 }
 
 hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {

@@ -141,10 +141,10 @@ struct ReplayRec {
   float eps = 0.f;
   _Float16* xn = nullptr;
   float* rec = nullptr;
-  // hybrid linear (Q8_K quantize + Q4_K x Q8_K): x, gamma, eps, n (tokens), D; weights, output
-  const uint8_t *hw0 = nullptr, *hw1 = nullptr;
-  uint8_t* x8 = nullptr;
-  int hN = 0, hK = 0, ldo = 0;
+  // hybrid linear (Q8_K quantize into the matrix-core operands + Q4_K x Q8_K GEMM): x, gamma,
+  // eps, n (tokens), D for the quantizer; ga / plan for the GEMM (epi: EPI_GATED or EPI_F32)
+  float* hd8 = nullptr;
+  _Float16* hbs = nullptr;
 };
 
 struct StagingSlot {
@@ -496,17 +496,35 @@ bool fold_norm(const t5h_model* m, int T) {
 }
 
 // Hybrid numerics (t5h_set_numerics): the FFN's gate|up and the projection quantize their f32
-// input to Q8_K and use integer Q4_K x Q8_K dot products.  The Q8_K rows live in the attention
-// output buffer `ao`, which is free once the O GEMM has consumed it (checked to fit at
-// t5h_set_numerics).  ln: the T5LayerNorm weight applied first (f32, from the residual x).
+// input to Q8_K and take Q4_K x Q8_K integer dot products on the matrix cores.  The quantizer
+// writes the integers as the f16 GEMM operand into the operand buffer `xn` (free after the QKV
+// GEMM) and the block scales and bsum operand into the attention output buffer `ao` (free once
+// the O GEMM has consumed it; checked to fit at t5h_set_numerics).  ln: the T5LayerNorm weight
+// applied first (f32, from the residual x).
 int hybrid_linear(t5h_model* m, int kind, const float* ln, const Linear& W0, const Linear* W1, int T, float* outf,
                   int ldo) {
   const t5h_config& c = m->cfg;
-  uint8_t* x8 = (uint8_t*)m->w.ao;
+  const int nblk = c.d_model / QK_K;
+  float* d8 = (float*)m->w.ao;
+  _Float16* bs = (_Float16*)((uint8_t*)m->w.ao + align256((size_t)m->w.tpad * nblk * 4));
   Timed t(m, kind, 2.0 * T * W0.N * W0.K * (W1 ? 2 : 1), 0);
-  HIP_OK(t5k::launch_q8k_quantize(m->w.x, ln, c.layer_norm_epsilon, T, c.d_model, x8, m->stream));
-  HIP_OK(t5k::launch_q4k_q8k((const uint8_t*)W0.w, W1 ? (const uint8_t*)W1->w : nullptr, x8, T, W0.N, W0.K, outf, ldo,
-                             W1 ? m->w.hb : nullptr, m->stream));
+  HIP_OK(t5k::launch_q8k_quantize(m->w.x, ln, c.layer_norm_epsilon, T, c.d_model, nullptr, m->stream, m->w.xn, d8,
+                                  bs));
+  GemmArgs a{};
+  a.A = m->w.xn;
+  a.W0 = W0.w;
+  a.W1 = W1 ? W1->w : nullptr;
+  a.M = T;
+  a.N = W0.N;
+  a.K = W0.K;
+  a.out = W1 ? (void*)m->w.hb : (void*)outf;
+  a.ldo = W1 ? W0.N : ldo;
+  a.tpad = m->w.tpad;
+  a.d8 = d8;
+  a.bsop = bs;
+  const int epi = W1 ? EPI_GATED : EPI_F32;
+  const t5k::GemmPlan plan = t5k::gemm_plan_hybrid(T, W0.N * (W1 ? 2 : 1), m->cus);
+  HIP_OK(t5k::launch_gemm_hybrid(epi, plan, a, m->stream));
   if (m->prof) {
     ReplayRec& r = m->replay[kind];
     r.type = ReplayRec::HYBRID;
@@ -515,14 +533,12 @@ int hybrid_linear(t5h_model* m, int kind, const float* ln, const Linear& W0, con
     r.eps = c.layer_norm_epsilon;
     r.n = T;
     r.D = c.d_model;
-    r.x8 = x8;
-    r.hw0 = (const uint8_t*)W0.w;
-    r.hw1 = W1 ? (const uint8_t*)W1->w : nullptr;
-    r.hN = W0.N;
-    r.hK = W0.K;
-    r.y = outf;
-    r.ldo = ldo;
-    r.xn = W1 ? m->w.hb : nullptr;
+    r.xn = m->w.xn;
+    r.hd8 = d8;
+    r.hbs = bs;
+    r.epi = epi;
+    r.ga = a;
+    r.plan = plan;
   }
   return T5H_OK;
 }
@@ -1524,8 +1540,10 @@ int t5h_set_numerics(t5h_model* m, int32_t mode) {
   if (m->proj.fmt != WF_Q4K) return fail(T5H_ERR_INVALID, "hybrid numerics: linear.weight must be Q4_K (QTiledOp)");
   if (c.d_model % QK_K || c.d_model > 1024 || c.d_ff % 64 || c.proj_dim % 64)
     return fail(T5H_ERR_INVALID, "hybrid numerics: needs d_model % 256 == 0 (<= 1024), d_ff and proj_dim % 64 == 0");
-  if ((size_t)t5k::q8k_bytes_per_row(c.d_model) > (size_t)m->inner * 2)
-    return fail(T5H_ERR_INVALID, "hybrid numerics: Q8_K rows do not fit the attention output buffer");
+  // block scales (4 B) and bsum operand (64 B) per token and K block in the attention output buffer
+  // (inner f16 per token; 2 B per token cover the alignment between the two, as tpad >= 128)
+  if ((size_t)(c.d_model / QK_K) * 68 + 2 > (size_t)m->inner * 2)
+    return fail(T5H_ERR_INVALID, "hybrid numerics: the Q8_K scales do not fit the attention output buffer");
   HIP_OK(hipStreamSynchronize(m->stream));
   m->numerics = mode;
   return T5H_OK;
@@ -1563,21 +1581,44 @@ int t5h_q8k_quantize(int32_t hip_device, const float* x, int32_t rows, int32_t c
 
 int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const uint8_t* x8, int32_t T, int32_t K,
                        float* out) {
-  if (N < 0 || T < 0 || K <= 0 || K % QK_K || N % 4) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: bad shape");
+  if (N < 0 || T < 0 || K <= 0 || K % QK_K || K > 1024 || N % 64)
+    return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: bad shape (K % 256 == 0, K <= 1024, N % 64 == 0)");
   if (N == 0 || T == 0) return T5H_OK;
   if (!w || !x8 || !out) return fail(T5H_ERR_INVALID, "q4k_q8k_matmul: NULL buffer");
   HIP_OK(hipSetDevice(hip_device));
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, hip_device);
+  // the GEMM's tiles read operand rows up to a whole tile past T
+  const int tpad = (T + 255) / 256 * 256, nblk = K / QK_K;
   const size_t wb = (size_t)N * K / QK_K * Q4K_BYTES, x8b = (size_t)T * t5k::q8k_bytes_per_row(K),
+               xqb = (size_t)tpad * K * 2, d8b = (size_t)tpad * nblk * 4, bsb = (size_t)tpad * nblk * 64,
                ob = (size_t)T * N * 4;
   void* d = nullptr;
-  if (hipMalloc(&d, align256(wb) + align256(x8b) + ob) != hipSuccess)
-    return fail(T5H_ERR_NOMEM, "q4k_q8k_matmul buffers");
+  const size_t total = align256(wb) + align256(x8b) + align256(xqb) + align256(d8b) + align256(bsb) + ob;
+  if (hipMalloc(&d, total) != hipSuccess) return fail(T5H_ERR_NOMEM, "q4k_q8k_matmul buffers");
   uint8_t* dw = (uint8_t*)d;
   uint8_t* dx = dw + align256(wb);
-  float* dout = (float*)(dx + align256(x8b));
-  hipError_t e = hipMemcpy(dw, w, wb, hipMemcpyHostToDevice);
+  _Float16* xq = (_Float16*)(dx + align256(x8b));
+  float* d8 = (float*)((uint8_t*)xq + align256(xqb));
+  _Float16* bs = (_Float16*)((uint8_t*)d8 + align256(d8b));
+  float* dout = (float*)((uint8_t*)bs + align256(bsb));
+  hipError_t e = hipMemset(d, 0, total);  // padding rows of the operands: zeros
+  if (e == hipSuccess) e = hipMemcpy(dw, w, wb, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(dx, x8, x8b, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = t5k::launch_q4k_q8k(dw, nullptr, dx, T, N, K, dout, N, nullptr, nullptr);
+  if (e == hipSuccess) e = t5k::launch_q8k_operands(dx, T, K, xq, d8, bs, nullptr);
+  if (e == hipSuccess) {
+    GemmArgs a{};
+    a.A = xq;
+    a.W0 = dw;
+    a.M = T;
+    a.N = N;
+    a.K = K;
+    a.out = dout;
+    a.ldo = N;
+    a.d8 = d8;
+    a.bsop = bs;
+    e = t5k::launch_gemm_hybrid(EPI_F32, t5k::gemm_plan_hybrid(T, N, cus), a, nullptr);
+  }
   if (e == hipSuccess) e = hipMemcpy(out, dout, ob, hipMemcpyDeviceToHost);
   (void)hipFree(d);
   if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("q4k_q8k_matmul: ") + hipGetErrorString(e));
@@ -1618,9 +1659,10 @@ int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) 
       case ReplayRec::RMSNORM:
         return t5k::launch_rmsnorm(r.x, r.gamma, r.xn, r.n, r.D, r.eps, m->stream, r.rec, r.rec_stride);
       case ReplayRec::HYBRID: {
-        const hipError_t e = t5k::launch_q8k_quantize(r.x, r.gamma, r.eps, r.n, r.D, r.x8, m->stream);
+        const hipError_t e =
+            t5k::launch_q8k_quantize(r.x, r.gamma, r.eps, r.n, r.D, nullptr, m->stream, r.xn, r.hd8, r.hbs);
         if (e != hipSuccess) return e;
-        return t5k::launch_q4k_q8k(r.hw0, r.hw1, r.x8, r.n, r.hN, r.hK, r.y, r.ldo, r.xn, m->stream);
+        return t5k::launch_gemm_hybrid(r.epi, r.plan, r.ga, m->stream);
       }
       default: return hipErrorInvalidValue;
     }
