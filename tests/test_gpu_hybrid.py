@@ -181,3 +181,48 @@ def test_set_numerics_rejects_non_q4k_ffn(enc):
             gpu.set_numerics(7)
     finally:
         gpu.close()
+
+
+def test_q4k_q8k_matmul_multi_tile_vs_oracle(enc):
+    """The matrix-core product over several token tiles and a thin tail (T = 300) and 512 weight
+    rows, against the oracle's vec_dot per (row, token) within 1e-6 of sum |terms|."""
+    rng = np.random.default_rng(70)
+    K, N, T = 768, 512, 300
+    w = quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x8 = enc.q8k_quantize((rng.standard_normal((T, K)) * rng.uniform(0.1, 10.0, (T, 1))).astype(np.float32))
+    got = enc.q4k_q8k_matmul(w, x8, K)
+    ts = rng.choice(T, 40, replace=False)
+    want = np.array([[orc.q4k_q8k_vec_dot(K, w[n], x8[t]) for n in range(N)] for t in ts], np.float32)
+    wd = orc.q4k_dequant(w).reshape(N, K).astype(np.float64)
+    xd = np.stack([_q8k_dequant(x8[t]) for t in ts])
+    scale = np.abs(xd) @ np.abs(wd).T
+    assert np.all(np.abs(got[ts] - want) <= 1e-6 * scale + 1e-30)
+
+
+def test_hybrid_batch_properties(enc):
+    """Hybrid numerics on a ragged batch that spans several tile rows of the hybrid GEMM (lengths
+    16..512, 20 sequences): finite, deterministic, sequences encoded alone bit-identical to their
+    rows in the batch (every tile plan keeps the K order), and sampled sequences against the
+    oracle's hybrid variant."""
+    cfg = dict(synth.XTR_BASE)
+    img = synth.make_model(cfg, seed=71, layout="hybrid")
+    gpu = enc.T5EncoderModel.from_gguf(img, cfg)
+    try:
+        gpu.set_numerics(1)
+        ids, cu = synth.ragged_batch(20, 16, 512, cfg["vocab_size"], seed=72)
+        out, _ = gpu.encode_packed(ids, cu)
+        assert np.isfinite(out).all()
+        out2, _ = gpu.encode_packed(ids, cu)
+        assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+        lens = np.diff(cu)
+        long = [int(b) for b in np.argsort(-lens)[:3]] + [int(b) for b in np.where(lens > 64)[0][:3]]
+        for b in sorted(set(long)):
+            s, e = int(cu[b]), int(cu[b + 1])
+            alone, _ = gpu.encode_packed(ids[s:e], np.array([0, e - s], np.int32))
+            assert np.array_equal(alone.view(np.uint32), out[s:e].view(np.uint32)), (b, e - s)
+        ora = orc.OracleModel(img, cfg, variant=orc.VARIANT_HYBRID)
+        for b in (int(np.argmax(lens)), int(np.argmin(lens))):
+            s, e = int(cu[b]), int(cu[b + 1])
+            assert _cos_rows(out[s:e], ora.forward(ids[s:e])).min() >= 0.999, (b, e - s)
+    finally:
+        gpu.close()
