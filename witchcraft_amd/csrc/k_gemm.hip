@@ -708,13 +708,14 @@ double list_makespan(int main, int tail, double c, int slots) {
 
 namespace t5k {
 // Tile choice for C[M, N]: 64*mw token rows (mw in {2, 4}) x bn weight rows (64 or 128).
-// Prefer the 4-math-wave x 128-row tile once it yields >= 1.4 tiles per CU; then the
-// 4 x 64 tile while it still covers >= 0.75 of the CUs; otherwise 2 x 64 (small token
-// counts, where latency dominates).  n_rows = weight rows of the launch (both matrices
-// for the gated FFN).
+// Prefer the 4-math-wave x 128-row tile once it fills at least one round of the CUs (the
+// thin tail tiles of gemm_plan spread a partial last round; cfg2 QKV, 324 tiles: 26.0 -> 24.7
+// us against 64-row tiles); then the 4 x 64 tile while it still covers >= 0.75 of the CUs;
+// otherwise 2 x 64 (small token counts, where latency dominates).  n_rows = weight rows of
+// the launch (both matrices for the gated FFN).
 void gemm_pick_tile(int M, int n_rows, int cus, int& mw, int& bn) {
   auto tiles = [&](int w, int b) { return (double)((M + 64 * w - 1) / (64 * w)) * (n_rows / b); };
-  if (n_rows % 128 == 0 && tiles(4, 128) >= 1.4 * cus) {
+  if (n_rows % 128 == 0 && tiles(4, 128) >= cus) {
     mw = 4;
     bn = 128;
   } else if (tiles(4, 64) >= 0.75 * cus) {
