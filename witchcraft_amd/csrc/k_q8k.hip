@@ -9,7 +9,7 @@
 // (row, token); the gate goes through a Pade tanh gelu (:128-133,168-170).  This is the
 // numerics of the reference's x86 default build.
 //
-//  * q8k_quantize_kernel: one workgroup per token, one wave per 256-value block (D <= 1024).
+//  * q8k_quantize_kernel: one wave per token, four tokens per workgroup (D <= 1024).
 //    Optional T5LayerNorm first (x / sqrt(mean(x^2) + eps) * w in f32, src/quantized_t5.rs:
 //    162-173).  Q8_K: the value of largest magnitude (the first one on ties) sets
 //    iscale = -128 / v, q = min(127, round(iscale * x)) with halves away from zero, d = 1 / iscale,
@@ -57,66 +57,80 @@ __device__ __forceinline__ void q8k_store_operands(const int (&q)[4], float d, i
   if ((lane & 3) == 1) blk[((2 + (g >> 3)) * 16 + (t & 15)) * 8 + (g & 7)] = (_Float16)0.f;
 }
 
+// One wave per token (four tokens per workgroup), all of the token's blocks in registers: lane l
+// holds values 4 l .. 4 l + 3 of every block, so the norm's and each block's reductions are wave
+// shuffles only.  The norm's sum of squares is added in the order of the one-wave-per-block form
+// (per block: lane pairs, then lanes by xor; then blocks (0 + 1) + (2 + 3)).
 __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
                                                            float eps, int T, int D, uint8_t* __restrict__ out,
                                                            _Float16* __restrict__ xq, float* __restrict__ d8,
                                                            _Float16* __restrict__ bsop) {
-  const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
   const int nb = D / 256;
-  __shared__ float part[4];
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  if (wave < nb) {
-    const float4 u = *reinterpret_cast<const float4*>(x + (size_t)t * D + 4 * tid);
-    v[0] = u.x, v[1] = u.y, v[2] = u.z, v[3] = u.w;
+  float v[4][4];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    float4 u = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b < nb) u = *reinterpret_cast<const float4*>(x + (size_t)t * D + 256 * b + 4 * lane);
+    v[b][0] = u.x, v[b][1] = u.y, v[b][2] = u.z, v[b][3] = u.w;
   }
   if (gamma) {  // T5LayerNorm in f32
-    float ss = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+    float part[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if (lane == 0) part[wave] = ss;
-    __syncthreads();
+    for (int b = 0; b < 4; b++) {
+      float ss = (v[b][0] * v[b][0] + v[b][1] * v[b][1]) + (v[b][2] * v[b][2] + v[b][3] * v[b][3]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      part[b] = ss;
+    }
     const float tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float den = sqrtf(tot / (float)D + eps);
-    if (wave < nb) {
-      const float4 g = *reinterpret_cast<const float4*>(gamma + 4 * tid);
-      v[0] = (v[0] / den) * g.x;
-      v[1] = (v[1] / den) * g.y;
-      v[2] = (v[2] / den) * g.z;
-      v[3] = (v[3] / den) * g.w;
-    }
-  }
-  if (wave >= nb) return;
-  // largest magnitude, first index on ties (the block's values in index order 4 * lane + i)
-  float a = fabsf(v[0]), mv = v[0];
-  int idx = 4 * lane;
 #pragma unroll
-  for (int i = 1; i < 4; i++)
-    if (fabsf(v[i]) > a) {
-      a = fabsf(v[i]);
-      mv = v[i];
-      idx = 4 * lane + i;
-    }
-  wave_absmax_first(a, idx, mv);
-  int q[4] = {0, 0, 0, 0};
-  float d = 0.f;
-  if (a != 0.f) {
-    const float iscale = -128.f / mv;
+    for (int b = 0; b < 4; b++)
+      if (b < nb) {
+        const float4 g = *reinterpret_cast<const float4*>(gamma + 256 * b + 4 * lane);
+        v[b][0] = (v[b][0] / den) * g.x;
+        v[b][1] = (v[b][1] / den) * g.y;
+        v[b][2] = (v[b][2] / den) * g.z;
+        v[b][3] = (v[b][3] / den) * g.w;
+      }
+  }
 #pragma unroll
-    for (int i = 0; i < 4; i++) q[i] = min(127, (int)roundf(iscale * v[i]));
-    d = 1.f / iscale;
+  for (int b = 0; b < 4; b++) {
+    if (b >= nb) break;
+    // largest magnitude, first index on ties (the block's values in index order 4 * lane + i)
+    float a = fabsf(v[b][0]), mv = v[b][0];
+    int idx = 4 * lane;
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+      if (fabsf(v[b][i]) > a) {
+        a = fabsf(v[b][i]);
+        mv = v[b][i];
+        idx = 4 * lane + i;
+      }
+    wave_absmax_first(a, idx, mv);
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.f;
+    if (a != 0.f) {
+      const float iscale = -128.f / mv;
+#pragma unroll
+      for (int i = 0; i < 4; i++) q[i] = min(127, (int)roundf(iscale * v[b][i]));
+      d = 1.f / iscale;
+    }
+    int s = (q[0] + q[1]) + (q[2] + q[3]);  // 16-value group g = lanes 4g .. 4g+3
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if (out) {
+      uint8_t* blk = out + ((size_t)t * nb + b) * Q8K_BYTES;
+      const uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) |
+                              ((uint32_t)(q[2] & 255) << 16) | ((uint32_t)(q[3] & 255) << 24);
+      *reinterpret_cast<uint32_t*>(blk + 4 + 4 * lane) = packed;
+      if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
+      if (lane == 0) *reinterpret_cast<float*>(blk) = d;
+    }
+    if (xq) q8k_store_operands(q, d, s, t, b, nb, D, lane, xq, d8, bsop);
   }
-  int s = (q[0] + q[1]) + (q[2] + q[3]);  // 16-value group g = lanes 4g .. 4g+3
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  if (out) {
-    uint8_t* blk = out + ((size_t)t * nb + wave) * Q8K_BYTES;
-    const uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) |
-                            ((uint32_t)(q[2] & 255) << 16) | ((uint32_t)(q[3] & 255) << 24);
-    *reinterpret_cast<uint32_t*>(blk + 4 + 4 * lane) = packed;
-    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *reinterpret_cast<float*>(blk) = d;
-  }
-  if (xq) q8k_store_operands(q, d, s, t, wave, nb, D, lane, xq, d8, bsop);
 }
 
 // Q8_K blocks [T][D/256] -> the matrix-core operands: one workgroup per token, one wave per block.
@@ -142,7 +156,7 @@ hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, in
                                hipStream_t s, _Float16* xq, float* d8, _Float16* bsop) {
   if (T <= 0) return hipSuccess;
   if (D <= 0 || D % QK_K || D > 1024 || (!out && !xq) || (xq && (!d8 || !bsop))) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(q8k_quantize_kernel, dim3(T), dim3(256), 0, s, x, gamma, eps, T, D, out, xq, d8, bsop);
+  hipLaunchKernelGGL(q8k_quantize_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gamma, eps, T, D, out, xq, d8, bsop);
   return hipGetLastError();
 }
 
