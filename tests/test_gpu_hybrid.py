@@ -226,3 +226,36 @@ def test_hybrid_batch_properties(enc):
             assert _cos_rows(out[s:e], ora.forward(ids[s:e])).min() >= 0.999, (b, e - s)
     finally:
         gpu.close()
+
+
+@pytest.mark.parametrize("lens", [[1], [7, 1, 33], [64, 65]])
+def test_hybrid_small_batches_vs_oracle(enc, lens):
+    """Hybrid numerics at query-sized and tiny batches (one partial tile of the hybrid GEMM; the
+    other linears on the GEMV kernels up to 64 tokens) against the oracle's hybrid variant."""
+    cfg = synth.small_config()
+    img = synth.make_model(cfg, seed=73)
+    gpu = enc.T5EncoderModel.from_gguf(img, cfg)
+    try:
+        gpu.set_numerics(1)
+        ora = orc.OracleModel(img, cfg, variant=orc.VARIANT_HYBRID)
+        cu = np.zeros(len(lens) + 1, np.int32)
+        cu[1:] = np.cumsum(lens)
+        ids = np.random.default_rng(74).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+        out, _ = gpu.encode_packed(ids, cu)
+        for b in range(len(lens)):
+            s, e = int(cu[b]), int(cu[b + 1])
+            assert _cos_rows(out[s:e], ora.forward(ids[s:e])).min() >= 0.999, (lens, b)
+    finally:
+        gpu.close()
+
+
+def test_q4k_q8k_matmul_single_token(enc):
+    rng = np.random.default_rng(75)
+    K, N = 256, 64
+    w = quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x8 = enc.q8k_quantize(rng.standard_normal((1, K)).astype(np.float32))
+    got = enc.q4k_q8k_matmul(w, x8, K)
+    want = np.array([[orc.q4k_q8k_vec_dot(K, w[n], x8[0]) for n in range(N)]], np.float32)
+    wd = orc.q4k_dequant(w).reshape(N, K).astype(np.float64)
+    scale = np.abs(_q8k_dequant(x8[0]))[None, :] @ np.abs(wd).T
+    assert np.all(np.abs(got - want) <= 1e-6 * scale + 1e-30)
