@@ -67,9 +67,10 @@ struct GemmArgs {
   const float* ngamma;
   // GEMV only: compute units of the device, for the grid shape (0: 256).
   int cus;
-  // Hybrid numerics (launch_gemm_hybrid): A holds the Q8_K integers q8 of every token as f16
-  // (exact), d8 [Mpad][K/256] their block scales, bsop the blocks' 16 bsums as the B operand of
-  // one 16x16x32 MFMA per (16-token row block, K block) -- 1 KiB blocks [Mpad/16][K/256], lane l
+  // Hybrid numerics (launch_gemm_hybrid): A holds the Q8_K integers q8 of every token as int8
+  // (blocks of 16 tokens x 64 K, 1 KiB, [Mpad/16][K/64]; lane l of a block: token l % 16, K
+  // 16 (l / 16) .. +15), d8 [Mpad][K/256] their block scales, bsop the blocks' 16 bsums as the
+  // B operand of one 16x16x32 MFMA per (16-token row block, K block) -- 1 KiB blocks [Mpad/16][K/256], lane l
   // = (token l % 16, K slots 8 (l / 16) .. +7): bsum 8 (l / 16) + e for l < 32, zero for l >= 32.
   const float* d8;
   const _Float16* bsop;
@@ -222,13 +223,13 @@ int embed_batch_blocks(int N);
 // xq null: not written).  launch_q8k_operands converts Q8_K blocks to those operands.
 int q8k_bytes_per_row(int D);
 hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, int T, int D, uint8_t* out,
-                               hipStream_t s, _Float16* xq = nullptr, float* d8 = nullptr, _Float16* bsop = nullptr);
-hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, _Float16* xq, float* d8, _Float16* bsop,
+                               hipStream_t s, int8_t* xq = nullptr, float* d8 = nullptr, _Float16* bsop = nullptr);
+hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, int8_t* xq, float* d8, _Float16* bsop,
                                hipStream_t s);
-// Q4_K weights x Q8_K activations on the matrix cores (k_gemm.hip): per K block of 256, f16(sc * q4)
-// against f16(q8) sums the block's integers in the f32 accumulator (exact below 2^24); the block
-// then adds d4 d8 * sum - dmin4 d8 * (mins . bsums) in f32.  epi: EPI_GATED (gelu_pade(W0) *
-// W1 into the f16 operand, operand order) or EPI_F32.  Q4_K weights, bn = 64, K <= 1024.
+// Q4_K weights x Q8_K activations on the matrix cores (k_gemm.hip): per K block of 256, the int8
+// planes (sc >> 3) q4 and (sc & 7) q4 against int8 q8 sum the block's integers exactly in int32
+// (8 hi + lo); the block then adds d4 d8 * sum - dmin4 d8 * (mins . bsums) in f32.  epi:
+// EPI_GATED (gelu_pade(W0) * W1 into the f16 operand, operand order) or EPI_F32.  Q4_K weights, bn = 64, K <= 1024.
 GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus);
 hipError_t launch_gemm_hybrid(int epi, const GemmPlan& plan, const GemmArgs& a, hipStream_t s);
 }  // namespace t5k

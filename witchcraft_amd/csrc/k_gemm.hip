@@ -126,15 +126,24 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
   }
 }
 
-// Hybrid numerics (launch_gemm_hybrid): the stage holds f16(sc * q) -- the sub-block scale times
-// the nibble, an integer <= 945, exact -- instead of the dequantized value (deq4 with the scale
-// 2^9 sc and no min: (q 2^-9)(sc 2^9) = sc q exactly).  At the first K step of a 256-wide block
-// the row's first producer thread also writes the block's d and dmin (Md) and its eight 6-bit
-// mins as the A operand of the min-term MFMA (Mm: m0 m0 m1 m1 .. m7 m7, one per bsum).
+// Hybrid numerics (launch_gemm_hybrid): the stage holds the nibbles times their sub-block scale
+// as two int8 planes.  A 6-bit scale splits as sc = 8 sh + sl (sh, sl <= 7), so sh q and sl q are
+// at most 105 and fit int8: the hi plane holds sh q, the lo plane sl q, and a K block's integer
+// sum is 8 (hi . q8) + (lo . q8), exact in int32.  Four nibbles masked into the bytes of a word
+// times a scale <= 7 give all four products with one multiply (no byte carries into the next).
+// Plane rows are 64 bytes (one K step); 16-byte chunk j of row r sits at chunk j ^ ((r >> 2) & 3),
+// so the math waves' fragment reads (16 rows x one chunk) hit every bank once.  At the first K
+// step of a 256-wide block the row's first producer thread also writes the block's d and dmin
+// (Md) and its eight 6-bit mins as the A operand of the min-term MFMA (Mm: m0 m0 m1 m1 .. m7 m7,
+// one per bsum).
+__device__ __forceinline__ int hyb_off(int r, int k) {  // byte offset of (row r, K index k) in a plane
+  return r * 64 + ((((k >> 4) ^ (r >> 2)) & 3) << 4) + (k & 15);
+}
 template <int NP, int BN>
 __device__ __forceinline__ void store_b_hybrid(const BRaw<WF_Q4K, NP, BN>& br, _Float16* Bs, float2* Md, h8* Mm,
                                                int kt, int pt) {
   using R = BRaw<WF_Q4K, NP, BN>;
+  static_assert(R::BPT == 8 || R::BPT == 16 || R::BPT == 32, "nibble bytes per thread");
   const int r = pt / R::TPR, part = pt % R::TPR;
   const int c = ((kt * BK) % QK_K) / 64;
   const uint4 hd = br.hd;
@@ -155,16 +164,21 @@ __device__ __forceinline__ void store_b_hybrid(const BRaw<WF_Q4K, NP, BN>& br, _
   int sc0, m0, sc1, m1;
   scale_min(2 * c, sc0, m0);
   scale_min(2 * c + 1, sc1, m1);
-  const float s0 = 512.0f * (float)sc0, s1 = 512.0f * (float)sc1;
+  uint8_t* hi = reinterpret_cast<uint8_t*>(Bs);
+  uint8_t* lo = hi + BN * 64;
+  // nibble word w holds values k0 + 4w .. +3 of sub-block 2c (low nibbles) and of 2c + 1 (high)
+  const int k0 = part * R::BPT;
 #pragma unroll
   for (int w = 0; w < R::NQ; w += 2) {
-    h4 lo0, hi0, lo1, hi1;
-    deq4(br.q[w], s0, 0.f, s1, 0.f, lo0, hi0);
-    deq4(br.q[w + 1], s0, 0.f, s1, 0.f, lo1, hi1);
-    *reinterpret_cast<h8*>(Bs + bswz(r, part * R::BPT + 4 * w)) =
-        h8{lo0[0], lo0[1], lo0[2], lo0[3], lo1[0], lo1[1], lo1[2], lo1[3]};
-    *reinterpret_cast<h8*>(Bs + bswz(r, 32 + part * R::BPT + 4 * w)) =
-        h8{hi0[0], hi0[1], hi0[2], hi0[3], hi1[0], hi1[1], hi1[2], hi1[3]};
+    const uint32_t l0 = br.q[w] & 0x0f0f0f0fu, l1 = br.q[w + 1] & 0x0f0f0f0fu;
+    const uint32_t h0 = (br.q[w] >> 4) & 0x0f0f0f0fu, h1 = (br.q[w + 1] >> 4) & 0x0f0f0f0fu;
+    const int k = k0 + 4 * w;
+    *reinterpret_cast<uint2*>(hi + hyb_off(r, k)) = make_uint2(l0 * (uint32_t)(sc0 >> 3), l1 * (uint32_t)(sc0 >> 3));
+    *reinterpret_cast<uint2*>(lo + hyb_off(r, k)) = make_uint2(l0 * (uint32_t)(sc0 & 7), l1 * (uint32_t)(sc0 & 7));
+    *reinterpret_cast<uint2*>(hi + hyb_off(r, 32 + k)) =
+        make_uint2(h0 * (uint32_t)(sc1 >> 3), h1 * (uint32_t)(sc1 >> 3));
+    *reinterpret_cast<uint2*>(lo + hyb_off(r, 32 + k)) =
+        make_uint2(h0 * (uint32_t)(sc1 & 7), h1 * (uint32_t)(sc1 & 7));
   }
   if (c == 0 && part == 0) {
     Md[r] = make_float2(f16_bits_to_f32(hd.x & 0xffff), f16_bits_to_f32(hd.x >> 16));
@@ -329,15 +343,20 @@ __device__ __forceinline__ float norm_factor(const GemmArgs& p, int mrow0, int n
   return inv / d.w;
 }
 
-// Math waves of a hybrid-numerics tile (launch_gemm_hybrid).  The stage holds f16(sc * q4) and the
-// A operand the Q8_K integers q8, so the MFMAs sum sc q4 q8 over a 256-wide K block exactly in the
-// f32 accumulator as long as partial sums stay below 2^24 (the sums' bound is 256 * 945 * 128;
-// quantized rows come nowhere near it, and beyond it the f32 sum is still within one unit in the
-// last place of the exact integer).  After its four K steps the block is folded into the output:
-//   out += (d4 d8) * sum  -  (dmin4 d8) * (mins . bsums),
-// the min term from one more MFMA of the row's mins (Mm) against the tokens' bsums (bsop).  This is
-// vec_dot's d * d8 * sum_j sc_j (q4 . q8)_j - dmin * d8 * sum_j m_j (bsum_2j + bsum_2j+1) per block
-// (src/fused_matmul.rs:36-41,147-172), with the f32 combination in this order.
+// Math waves of a hybrid-numerics tile (launch_gemm_hybrid).  The stage holds sc q4 as the int8
+// planes hi = (sc >> 3) q4 and lo = (sc & 7) q4 (store_b_hybrid) and the A operand the Q8_K
+// integers q8 as int8, so v_mfma_i32_16x16x64_i8 sums each plane against q8 exactly in int32, and
+// a 256-wide K block's integer sum is 8 hi + lo.  After its four K steps the block is folded into
+// the f32 output:
+//   out += (d4 d8) * float(sum)  -  (dmin4 d8) * (mins . bsums),
+// the min term from one f16 MFMA of the row's mins (Mm) against the tokens' bsums (bsop, exact:
+// <= 16 * 63 * 2048).  This is vec_dot's d * d8 * sum_j sc_j (q4 . q8)_j - dmin * d8 *
+// sum_j m_j (bsum_2j + bsum_2j+1) per block (src/fused_matmul.rs:36-41,147-172): the integer
+// sum is exact and converted to f32 once, as there.
+// A operand (p.A as bytes): blocks of 16 tokens x 64 K (1 KiB) [Mpad/16][K/64], lane l holding
+// token l % 16, K 16 (l / 16) .. +15; the weight fragment of lane l is row l % 16 of its row
+// block, the same 16 K values.
+typedef int v4i __attribute__((ext_vector_type(4)));
 template <int EPI, int MW, int BN, int S, int MB>
 __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK],
                                             const float2 (*Md)[BN], const h8 (*Mm)[2 * BN]) {
@@ -346,30 +365,32 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
   const int nkt = p.K / BK, nblk = p.K / QK_K;
   const int mrow0 = m0 + wave * 16 * MB;
-  const size_t kblk = p.K / 32;
-  const _Float16* ablk[MB];
+  const size_t kch = p.K / 64;  // 1 KiB operand blocks per 16-token row block
+  const uint8_t* ablk[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++) ablk[mb] = p.A + ((size_t)(mrow0 / 16 + mb) * kblk) * 512 + lane * 8;
+  for (int mb = 0; mb < MB; mb++)
+    ablk[mb] = reinterpret_cast<const uint8_t*>(p.A) + (size_t)(mrow0 / 16 + mb) * kch * 1024 + lane * 16;
 
-  f4 acc[MB][NB], out[MB][NB];
+  v4i acc_hi[MB][NB], acc_lo[MB][NB];
+  f4 out[MB][NB];
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
     for (int j = 0; j < NB; j++) out[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 a[S][MB][2];
-#define LOAD_A(st, kt)                                                                      \
-  _Pragma("unroll") for (int mb = 0; mb < MB; mb++) {                                        \
-    a[st][mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);     \
-    a[st][mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512); \
-  }
+  uint4 a[S][MB];
+#define LOAD_A(st, kt) \
+  _Pragma("unroll") for (int mb = 0; mb < MB; mb++) a[st][mb] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(kt) * 1024);
   LOAD_A(0, 0);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 
-  const _Float16* bbase0 = &Bs[0][bswz(lr, 8 * lg)];
-  const _Float16* bbase1 = &Bs[0][bswz(lr, 32 + 8 * lg)];
+  // this lane's fragment of row block nb: row 16 nb + lr, K chunk lg
+  int foff[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++) foff[nb] = hyb_off(16 * nb + lr, 16 * lg);
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  const v4i izero = {0, 0, 0, 0};
   for (int b = 0; b < nblk; b++) {
     // the block's d8 and bsum operand of every row block, requested before its MFMAs
     float d8v[MB];
@@ -384,22 +405,18 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
       const int kt = 4 * b + u;
       LOAD_A((u + 1) % S, min(kt + 1, nkt - 1));
       __builtin_amdgcn_sched_barrier(0);
-      const _Float16* bsrc0 = bbase0 + (kt & 1) * (BN * LDSK);
-      const _Float16* bsrc1 = bbase1 + (kt & 1) * (BN * LDSK);
-      constexpr int NF = 2 * NB, FD = 2;
-      h8 wf[FD + 1];
+      const uint8_t* hi = reinterpret_cast<const uint8_t*>(Bs[kt & 1]);
+      const uint8_t* lo = hi + BN * 64;
 #pragma unroll
-      for (int j = 0; j < FD; j++) wf[j] = *reinterpret_cast<const h8*>((j / NB ? bsrc1 : bsrc0) + (j % NB) * 16 * LDSK);
+      for (int nb = 0; nb < NB; nb++) {
+        const v4i wh = *reinterpret_cast<const v4i*>(hi + foff[nb]);
+        const v4i wl = *reinterpret_cast<const v4i*>(lo + foff[nb]);
 #pragma unroll
-      for (int j = 0; j < NF; j++) {
-        if (j + FD < NF)
-          wf[(j + FD) % (FD + 1)] =
-              *reinterpret_cast<const h8*>(((j + FD) / NB ? bsrc1 : bsrc0) + ((j + FD) % NB) * 16 * LDSK);
-        const int sk = j / NB, nb = j % NB;
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j % (FD + 1)], __builtin_bit_cast(h8, a[u % S][mb][sk]),
-                                                                (u == 0 && sk == 0) ? zero : acc[mb][nb], 0, 0, 0);
+        for (int mb = 0; mb < MB; mb++) {
+          const v4i x = __builtin_bit_cast(v4i, a[u % S][mb]);
+          acc_hi[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, x, u == 0 ? izero : acc_hi[mb][nb], 0, 0, 0);
+          acc_lo[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, x, u == 0 ? izero : acc_lo[mb][nb], 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       __syncthreads();
@@ -417,7 +434,8 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
         const f4 cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(mf, __builtin_bit_cast(h8, bsf[mb]), zero, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          out[mb][nb][i] = __builtin_fmaf(dd[i] * d8v[mb], acc[mb][nb][i], out[mb][nb][i]);
+          const float sum = (float)((acc_hi[mb][nb][i] << 3) + acc_lo[mb][nb][i]);
+          out[mb][nb][i] = __builtin_fmaf(dd[i] * d8v[mb], sum, out[mb][nb][i]);
           out[mb][nb][i] = __builtin_fmaf(-(dm[i] * d8v[mb]), cm[i], out[mb][nb][i]);
         }
       }

@@ -15,8 +15,8 @@
 //    iscale = -128 / v, q = min(127, round(iscale * x)) with halves away from zero, d = 1 / iscale,
 //    bsums = sums of 16 consecutive q; an all-zero block gives d = 0 and q = 0.  Bit-exact with
 //    BlockQ8K::from_float on the same f32 input.  Writes the Q8_K blocks and/or the operands of
-//    the matrix-core product: q as f16 in operand order (exact), d per block, and the bsums as
-//    the B operand of the min-term MFMA.
+//    the matrix-core product: q as the int8 operand of v_mfma_i32_16x16x64_i8, d per block, and
+//    the bsums as the B operand of the min-term MFMA.
 //  * q8k_operands_kernel: Q8_K blocks -> the same operands (the standalone matmul entry point).
 #include "common.hpp"
 
@@ -43,13 +43,17 @@ __device__ __forceinline__ void wave_absmax_first(float& a, int& idx, float& v) 
 
 // The matrix-core operands of one lane's four values q[0..3] (values 4 lane .. 4 lane + 3 of block
 // b of token t), the block scale d (lane 0) and the 16-value group sum s of lane 4g (the bsum of
-// group g = lane / 4): q into the f16 operand xq (operand order, 8 bytes), d into d8, bsum g into
-// its slot of the (t / 16, b) bsum operand block, and lanes 4g + 1 zero the slot of lane group
-// 2 + g / 8 (K slots 16..31 of the min-term MFMA, which have no bsum).
+// group g = lane / 4): q into the int8 operand xq (4 bytes; blocks of 16 tokens x 64 K, lane l of
+// a block holding token l % 16, K 16 (l / 16) .. +15), d into d8, bsum g into its slot of the
+// (t / 16, b) bsum operand block, and lanes 4g + 1 zero the slot of lane group 2 + g / 8 (K slots
+// 16..31 of the min-term MFMA, which have no bsum).
 __device__ __forceinline__ void q8k_store_operands(const int (&q)[4], float d, int s, int t, int b, int nb, int D,
-                                                   int lane, _Float16* xq, float* d8, _Float16* bsop) {
-  *reinterpret_cast<h4*>(xq + tiled_index(t, 256 * b + 4 * lane, D)) =
-      h4{(_Float16)q[0], (_Float16)q[1], (_Float16)q[2], (_Float16)q[3]};
+                                                   int lane, int8_t* xq, float* d8, _Float16* bsop) {
+  const int k = 256 * b + 4 * lane;
+  const uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+                          ((uint32_t)(q[3] & 255) << 24);
+  *reinterpret_cast<uint32_t*>(xq + ((size_t)(t >> 4) * (D / 64) + (k >> 6)) * 1024 +
+                               (((k & 63) >> 4) * 16 + (t & 15)) * 16 + (k & 15)) = packed;
   if (lane == 0) d8[(size_t)t * nb + b] = d;
   const int g = lane >> 2;
   _Float16* blk = bsop + ((size_t)(t >> 4) * nb + b) * 512;
@@ -63,7 +67,7 @@ __device__ __forceinline__ void q8k_store_operands(const int (&q)[4], float d, i
 // (per block: lane pairs, then lanes by xor; then blocks (0 + 1) + (2 + 3)).
 __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
                                                            float eps, int T, int D, uint8_t* __restrict__ out,
-                                                           _Float16* __restrict__ xq, float* __restrict__ d8,
+                                                           int8_t* __restrict__ xq, float* __restrict__ d8,
                                                            _Float16* __restrict__ bsop) {
   const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restri
 
 // Q8_K blocks [T][D/256] -> the matrix-core operands: one workgroup per token, one wave per block.
 __global__ __launch_bounds__(256) void q8k_operands_kernel(const uint8_t* __restrict__ blocks, int D,
-                                                           _Float16* __restrict__ xq, float* __restrict__ d8,
+                                                           int8_t* __restrict__ xq, float* __restrict__ d8,
                                                            _Float16* __restrict__ bsop) {
   const int t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = D / QK_K;
   if (wave >= nb) return;
@@ -153,14 +157,14 @@ namespace t5k {
 int q8k_bytes_per_row(int D) { return D / QK_K * Q8K_BYTES; }
 
 hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, int T, int D, uint8_t* out,
-                               hipStream_t s, _Float16* xq, float* d8, _Float16* bsop) {
+                               hipStream_t s, int8_t* xq, float* d8, _Float16* bsop) {
   if (T <= 0) return hipSuccess;
   if (D <= 0 || D % QK_K || D > 1024 || (!out && !xq) || (xq && (!d8 || !bsop))) return hipErrorInvalidValue;
   hipLaunchKernelGGL(q8k_quantize_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gamma, eps, T, D, out, xq, d8, bsop);
   return hipGetLastError();
 }
 
-hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, _Float16* xq, float* d8, _Float16* bsop,
+hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, int8_t* xq, float* d8, _Float16* bsop,
                                hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (D <= 0 || D % QK_K || D > 1024 || !blocks || !xq || !d8 || !bsop) return hipErrorInvalidValue;

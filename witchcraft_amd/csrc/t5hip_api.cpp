@@ -497,7 +497,7 @@ bool fold_norm(const t5h_model* m, int T) {
 
 // Hybrid numerics (t5h_set_numerics): the FFN's gate|up and the projection quantize their f32
 // input to Q8_K and take Q4_K x Q8_K integer dot products on the matrix cores.  The quantizer
-// writes the integers as the f16 GEMM operand into the operand buffer `xn` (free after the QKV
+// writes the integers as the int8 GEMM operand into the operand buffer `xn` (free after the QKV
 // GEMM) and the block scales and bsum operand into the attention output buffer `ao` (free once
 // the O GEMM has consumed it; checked to fit at t5h_set_numerics).  ln: the T5LayerNorm weight
 // applied first (f32, from the residual x).
@@ -508,10 +508,10 @@ int hybrid_linear(t5h_model* m, int kind, const float* ln, const Linear& W0, con
   float* d8 = (float*)m->w.ao;
   _Float16* bs = (_Float16*)((uint8_t*)m->w.ao + align256((size_t)m->w.tpad * nblk * 4));
   Timed t(m, kind, 2.0 * T * W0.N * W0.K * (W1 ? 2 : 1), 0);
-  HIP_OK(t5k::launch_q8k_quantize(m->w.x, ln, c.layer_norm_epsilon, T, c.d_model, nullptr, m->stream, m->w.xn, d8,
-                                  bs));
+  HIP_OK(t5k::launch_q8k_quantize(m->w.x, ln, c.layer_norm_epsilon, T, c.d_model, nullptr, m->stream,
+                                  reinterpret_cast<int8_t*>(m->w.xn), d8, bs));
   GemmArgs a{};
-  a.A = m->w.xn;
+  a.A = m->w.xn;  // the int8 operand blocks (GemmArgs::A, hybrid)
   a.W0 = W0.w;
   a.W1 = W1 ? W1->w : nullptr;
   a.M = T;
@@ -1591,14 +1591,14 @@ int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const ui
   // the GEMM's tiles read operand rows up to a whole tile past T
   const int tpad = (T + 255) / 256 * 256, nblk = K / QK_K;
   const size_t wb = (size_t)N * K / QK_K * Q4K_BYTES, x8b = (size_t)T * t5k::q8k_bytes_per_row(K),
-               xqb = (size_t)tpad * K * 2, d8b = (size_t)tpad * nblk * 4, bsb = (size_t)tpad * nblk * 64,
+               xqb = (size_t)tpad * K, d8b = (size_t)tpad * nblk * 4, bsb = (size_t)tpad * nblk * 64,
                ob = (size_t)T * N * 4;
   void* d = nullptr;
   const size_t total = align256(wb) + align256(x8b) + align256(xqb) + align256(d8b) + align256(bsb) + ob;
   if (hipMalloc(&d, total) != hipSuccess) return fail(T5H_ERR_NOMEM, "q4k_q8k_matmul buffers");
   uint8_t* dw = (uint8_t*)d;
   uint8_t* dx = dw + align256(wb);
-  _Float16* xq = (_Float16*)(dx + align256(x8b));
+  int8_t* xq = (int8_t*)(dx + align256(x8b));
   float* d8 = (float*)((uint8_t*)xq + align256(xqb));
   _Float16* bs = (_Float16*)((uint8_t*)d8 + align256(d8b));
   float* dout = (float*)((uint8_t*)bs + align256(bsb));
@@ -1608,7 +1608,7 @@ int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const ui
   if (e == hipSuccess) e = t5k::launch_q8k_operands(dx, T, K, xq, d8, bs, nullptr);
   if (e == hipSuccess) {
     GemmArgs a{};
-    a.A = xq;
+    a.A = reinterpret_cast<const _Float16*>(xq);  // int8 operand blocks (GemmArgs::A, hybrid)
     a.W0 = dw;
     a.M = T;
     a.N = N;
@@ -1660,7 +1660,8 @@ int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) 
         return t5k::launch_rmsnorm(r.x, r.gamma, r.xn, r.n, r.D, r.eps, m->stream, r.rec, r.rec_stride);
       case ReplayRec::HYBRID: {
         const hipError_t e =
-            t5k::launch_q8k_quantize(r.x, r.gamma, r.eps, r.n, r.D, nullptr, m->stream, r.xn, r.hd8, r.hbs);
+            t5k::launch_q8k_quantize(r.x, r.gamma, r.eps, r.n, r.D, nullptr, m->stream,
+                                     reinterpret_cast<int8_t*>(r.xn), r.hd8, r.hbs);
         if (e != hipSuccess) return e;
         return t5k::launch_gemm_hybrid(r.epi, r.plan, r.ga, m->stream);
       }
