@@ -136,6 +136,8 @@ __device__ __forceinline__ void store_b(const BRaw<WF, NP, BN>& br, _Float16* Bs
 // step of a 256-wide block the row's first producer thread also writes the block's d and dmin
 // (Md) and its eight 6-bit mins as the A operand of the min-term MFMA (Mm: m0 m0 m1 m1 .. m7 m7,
 // one per bsum).
+// 16-token row blocks per math wave in a full hybrid tile (the tile is 16 HYB_MB MW tokens).
+constexpr int HYB_MB = 3;
 __device__ __forceinline__ int hyb_off(int r, int k) {  // byte offset of (row r, K index k) in a plane
   return r * 64 + ((((k >> 4) ^ (r >> 2)) & 3) << 4) + (k & 15);
 }
@@ -343,23 +345,25 @@ __device__ __forceinline__ float norm_factor(const GemmArgs& p, int mrow0, int n
   return inv / d.w;
 }
 
-// Math waves of a hybrid-numerics tile (launch_gemm_hybrid).  The stage holds sc q4 as the int8
-// planes hi = (sc >> 3) q4 and lo = (sc & 7) q4 (store_b_hybrid) and the A operand the Q8_K
-// integers q8 as int8, so v_mfma_i32_16x16x64_i8 sums each plane against q8 exactly in int32, and
-// a 256-wide K block's integer sum is 8 hi + lo.  After its four K steps the block is folded into
-// the f32 output:
-//   out += (d4 d8) * float(sum)  -  (dmin4 d8) * (mins . bsums),
+// Hybrid-numerics tile (launch_gemm_hybrid).  The stage holds sc q4 as the int8 planes
+// hi = (sc >> 3) q4 and lo = (sc & 7) q4 (store_b_hybrid) and the A operand the Q8_K integers q8
+// as int8, so v_mfma_i32_16x16x64_i8 sums each plane against q8 exactly in int32, and a 256-wide
+// K block's integer sum is S = 8 hi + lo.  The block is then folded into the f32 output:
+//   out += d8 * (d4 * float(S) - dmin4 * (mins . bsums)),
 // the min term from one f16 MFMA of the row's mins (Mm) against the tokens' bsums (bsop, exact:
 // <= 16 * 63 * 2048).  This is vec_dot's d * d8 * sum_j sc_j (q4 . q8)_j - dmin * d8 *
 // sum_j m_j (bsum_2j + bsum_2j+1) per block (src/fused_matmul.rs:36-41,147-172): the integer
 // sum is exact and converted to f32 once, as there.
+// The math waves only run the integer MFMAs: at a block's last K step each writes its S tiles to
+// the exchange buffer Sx, and producer wave MW + w folds math wave w's block during the next
+// block's first K step (HybFold), so the fold's VALU work overlaps the next block's MFMAs on the
+// same SIMD instead of stalling them.  Sx is read three barriers before it is written again.
 // A operand (p.A as bytes): blocks of 16 tokens x 64 K (1 KiB) [Mpad/16][K/64], lane l holding
 // token l % 16, K 16 (l / 16) .. +15; the weight fragment of lane l is row l % 16 of its row
-// block, the same 16 K values.
+// block, the same 16 K values.  Sx: [MW][MB][NB][64 lanes] int4, the lane's four outputs.
 typedef int v4i __attribute__((ext_vector_type(4)));
 template <int EPI, int MW, int BN, int S, int MB>
-__device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK],
-                                            const float2 (*Md)[BN], const h8 (*Mm)[2 * BN]) {
+__device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, _Float16 (*Bs)[BN * LDSK], int4* Sx) {
   constexpr int NB = BN / 16;
   static_assert(S == 2, "the hybrid loop unrolls a K block as two A stages");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
@@ -370,14 +374,9 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
 #pragma unroll
   for (int mb = 0; mb < MB; mb++)
     ablk[mb] = reinterpret_cast<const uint8_t*>(p.A) + (size_t)(mrow0 / 16 + mb) * kch * 1024 + lane * 16;
+  int4* sx = Sx + (size_t)wave * MB * NB * 64 + lane;
 
   v4i acc_hi[MB][NB], acc_lo[MB][NB];
-  f4 out[MB][NB];
-#pragma unroll
-  for (int i = 0; i < MB; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) out[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
   uint4 a[S][MB];
 #define LOAD_A(st, kt) \
   _Pragma("unroll") for (int mb = 0; mb < MB; mb++) a[st][mb] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(kt) * 1024);
@@ -389,17 +388,8 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
   int foff[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; nb++) foff[nb] = hyb_off(16 * nb + lr, 16 * lg);
-  const f4 zero = {0.f, 0.f, 0.f, 0.f};
   const v4i izero = {0, 0, 0, 0};
   for (int b = 0; b < nblk; b++) {
-    // the block's d8 and bsum operand of every row block, requested before its MFMAs
-    float d8v[MB];
-    uint4 bsf[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-      d8v[mb] = p.d8[(size_t)(mrow0 + 16 * mb + lr) * nblk + b];
-      bsf[mb] = *reinterpret_cast<const uint4*>(p.bsop + ((size_t)(mrow0 / 16 + mb) * nblk + b) * 512 + lane * 8);
-    }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int kt = 4 * b + u;
@@ -419,10 +409,58 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if (u == 3) {
+        // block b's sums for the fold waves: lane holds rows 16nb + 4lg + i of token 16mb + lr
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+          for (int nb = 0; nb < NB; nb++) {
+            const v4i sum = (acc_hi[mb][nb] << 3) + acc_lo[mb][nb];
+            sx[(mb * NB + nb) * 64] = make_int4(sum[0], sum[1], sum[2], sum[3]);
+          }
+      }
       __syncthreads();
     }
-    // fold block b: lane holds rows n0 + 16nb + 4lg + i of token mrow0 + 16mb + lr
+  }
+#undef LOAD_A
+}
+
+// Producer wave MW + w's share of a hybrid tile: the f32 outputs of math wave w, folded block by
+// block from Sx, and the epilogue.
+template <int EPI, int MW, int BN, int MB>
+struct HybFold {
+  static constexpr int NB = BN / 16;
+  f4 out[MB][NB];
+  float d8v[MB];  // the next block's d8 and bsum operand, requested a block ahead
+  uint4 bsf[MB];
+  int mrow0, lane, lr, lg, nblk;
+  const int4* sx;
+
+  __device__ __forceinline__ void load_meta(const GemmArgs& p, int b) {
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      d8v[mb] = p.d8[(size_t)(mrow0 + 16 * mb + lr) * nblk + b];
+      bsf[mb] = *reinterpret_cast<const uint4*>(p.bsop + ((size_t)(mrow0 / 16 + mb) * nblk + b) * 512 + lane * 8);
+    }
+  }
+  __device__ __forceinline__ void init(const GemmArgs& p, int m0, const int4* Sx) {
+    const int w = (threadIdx.x >> 6) - MW;
+    lane = threadIdx.x & 63;
+    lr = lane & 15;
+    lg = lane >> 4;
+    nblk = p.K / QK_K;
+    mrow0 = m0 + w * 16 * MB;
+    sx = Sx + (size_t)w * MB * NB * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int j = 0; j < NB; j++) out[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    load_meta(p, 0);
+  }
+  // block b: its sums in Sx, its row metadata in Md / Mm [b % 2], its d8 / bsums in d8v / bsf
+  __device__ __forceinline__ void fold(const GemmArgs& p, int b, const float2 (*Md)[BN], const h8 (*Mm)[2 * BN]) {
     const int bp = b & 1;
+    const f4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
       const float4 q0 = *reinterpret_cast<const float4*>(&Md[bp][16 * nb + 4 * lg]);
@@ -432,42 +470,47 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, int n0, _
 #pragma unroll
       for (int mb = 0; mb < MB; mb++) {
         const f4 cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(mf, __builtin_bit_cast(h8, bsf[mb]), zero, 0, 0, 0);
+        const int4 sv = sx[(mb * NB + nb) * 64];
+        const int si[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float sum = (float)((acc_hi[mb][nb][i] << 3) + acc_lo[mb][nb][i]);
-          out[mb][nb][i] = __builtin_fmaf(dd[i] * d8v[mb], sum, out[mb][nb][i]);
-          out[mb][nb][i] = __builtin_fmaf(-(dm[i] * d8v[mb]), cm[i], out[mb][nb][i]);
+          // d8 (d S - dmin M): the block's row scales first, the token's scale once
+          const float t = __builtin_fmaf(-dm[i], cm[i], dd[i] * (float)si[i]);
+          out[mb][nb][i] = __builtin_fmaf(d8v[mb], t, out[mb][nb][i]);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);  // one row block at a time: bounded live registers
     }
+    if (b + 1 < nblk) load_meta(p, b + 1);
   }
-#undef LOAD_A
-
+  __device__ __forceinline__ void epilogue(const GemmArgs& p, int n0) {
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++) {
-    const int m = mrow0 + mb * 16 + lr;
-    if (m >= p.M) continue;
-    if constexpr (EPI == EPI_GATED) {
+    for (int mb = 0; mb < MB; mb++) {
+      const int m = mrow0 + mb * 16 + lr;
+      if (m >= p.M) continue;
+      if constexpr (EPI == EPI_GATED) {
 #pragma unroll
-      for (int nb = 0; nb < NB / 2; nb++) {
-        const f4 g = out[mb][nb], v = out[mb][nb + NB / 2];
-        *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
-            h4{(_Float16)(gelu_pade(g[0]) * v[0]), (_Float16)(gelu_pade(g[1]) * v[1]),
-               (_Float16)(gelu_pade(g[2]) * v[2]), (_Float16)(gelu_pade(g[3]) * v[3])};
+        for (int nb = 0; nb < NB / 2; nb++) {
+          const f4 g = out[mb][nb], v = out[mb][nb + NB / 2];
+          *reinterpret_cast<h4*>((_Float16*)p.out + tiled_index(m, n0 + nb * 16 + 4 * lg, p.ldo)) =
+              h4{(_Float16)(gelu_pade(g[0]) * v[0]), (_Float16)(gelu_pade(g[1]) * v[1]),
+                 (_Float16)(gelu_pade(g[2]) * v[2]), (_Float16)(gelu_pade(g[3]) * v[3])};
+        }
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) store_quad<EPI_F32>(p, m, n0 + nb * 16 + 4 * lg, out[mb][nb]);
       }
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < NB; nb++) store_quad<EPI_F32>(p, m, n0 + nb * 16 + 4 * lg, out[mb][nb]);
     }
   }
-}
+};
 
 // One output tile: tokens [m0, m0 + 16*MB*MW) x weight rows from n0.  MB = 16-row operand
 // blocks per math wave: 4 for full tiles, 1 or 2 for the thin tiles that spread the last,
 // partial round of a launch over every CU (the weight stage per K step is the same).
 template <int EPI, int WF, int MW, int BN, int S, int MB, bool HY = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Float16 (*Bs)[BN * LDSK],
-                                          float2 (*Md)[BN] = nullptr, h8 (*Mm)[2 * BN] = nullptr) {
+                                          float2 (*Md)[BN] = nullptr, h8 (*Mm)[2 * BN] = nullptr,
+                                          int4* Sx = nullptr) {
   constexpr int NP = 64 * MW, NB = BN / 16;
   // S register stages of A (math waves) and PB of raw weights (producers): the loads of a
   // step are issued S-1 (PB-1) steps before it is consumed, covering L2/MALL latency.
@@ -493,6 +536,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
     store(br[0], 0);
 #pragma unroll
     for (int i = 1; i < PB; i++) load_b<EPI, WF, NP, BN>(br[i], p, n0, i, pt);
+    // hybrid numerics: these waves also fold the math waves' block sums (PB steps = one block)
+    HybFold<EPI, MW, BN, MB> hf;
+    if constexpr (HY) {
+      static_assert(PB * BK == QK_K, "one producer ring turn per Q4_K block");
+      hf.init(p, m0, Sx);
+    }
     __syncthreads();
     // nkt % PB == 0 (K % 256 == 0); loads past the last step re-read it (in bounds, unused)
     // so that every load is unconditional and the compiler's wait counts stay exact.
@@ -502,15 +551,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
         const int kt = kt0 + u;
         if (kt + 1 < nkt) store(br[(u + 1) % PB], kt + 1);
         load_b<EPI, WF, NP, BN>(br[u], p, n0, min(kt + PB, nkt - 1), pt);
+        if constexpr (HY)
+          if (u == 0 && kt0 > 0) hf.fold(p, kt0 / PB - 1, Md, Mm);
         __syncthreads();
       }
+    }
+    if constexpr (HY) {
+      hf.fold(p, nkt / PB - 1, Md, Mm);
+      hf.epilogue(p, n0);
     }
     return;
   }
 
   // -------------------------------- math waves ---------------------------------
   if constexpr (HY) {
-    math_hybrid<EPI, MW, BN, S, MB>(p, m0, n0, Bs, Md, Mm);
+    math_hybrid<EPI, MW, BN, S, MB>(p, m0, Bs, Sx);
     return;
   }
   const int lr = lane & 15, lg = lane >> 4;
@@ -634,17 +689,19 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
   // hybrid numerics: per-row block metadata (d, dmin; mins as an MFMA operand), two blocks deep
   __shared__ __attribute__((aligned(16))) float2 Md[HY ? 2 : 1][HY ? BN : 1];
   __shared__ __attribute__((aligned(16))) h8 Mm[HY ? 2 : 1][HY ? 2 * BN : 1];
+  // hybrid numerics: the math waves' block sums for the fold waves
+  __shared__ int4 Sx[HY ? MW * HYB_MB * (BN / 16) * 64 : 1];
   constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN;  // output columns per tile
-  // Full tiles: 4 row blocks per math wave; 2 with hybrid numerics, whose waves hold a second set
-  // of accumulators (the block sums next to the output).
-  constexpr int MBM = HY ? 2 : 4;
+  // Full tiles: 4 row blocks per math wave; HYB_MB with hybrid numerics, whose math waves hold
+  // two int32 accumulator sets (the planes' block sums).
+  constexpr int MBM = HY ? HYB_MB : 4;
   int b = blockIdx.x;
   if (TMB == 0 || b < g.main_blocks) {
     const int tile = (b % 8) * (g.main_blocks / 8) + b / 8;
     if (tile >= g.main_tiles) return;
     if constexpr (HY)
       gemm_tile<EPI, WF, MW, BN, S, MBM, true>(p, (tile / g.tiles_n) * 16 * MBM * MW, (tile % g.tiles_n) * cols, Bs,
-                                               Md, Mm);
+                                               Md, Mm, Sx);
     else
       gemm_tile<EPI, WF, MW, BN, S, 4>(p, (tile / g.tiles_n) * 64 * MW, (tile % g.tiles_n) * cols, Bs);
   } else {
@@ -654,7 +711,7 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
     if (tile >= g.tail_tiles) return;
     if constexpr (HY)
       gemm_tile<EPI, WF, MW, BN, S, MBT, true>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
-                                               (tile % g.tiles_n) * cols, Bs, Md, Mm);
+                                               (tile % g.tiles_n) * cols, Bs, Md, Mm, Sx);
     else
       gemm_tile<EPI, WF, MW, BN, S, MBT>(p, g.m_main + (tile / g.tiles_n) * 16 * MBT * MW,
                                           (tile % g.tiles_n) * cols, Bs);
@@ -663,7 +720,7 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
 
 template <int EPI, int WF, int BN, int S, int MW, int TMB, bool HY = false>
 hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
-  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = (HY ? 32 : 64) * MW;
+  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = (HY ? 16 * HYB_MB : 64) * MW;
   GemmGrid g;
   g.tiles_n = a.N / cols;
   g.m_main = TMB ? pl.m_main : a.M;
@@ -797,7 +854,7 @@ GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus) {
   pl.mw = 4;
   pl.m_main = M;
   pl.tail_mb = 0;
-  const int bm = 128, tiles_n = n_rows / 64, full = (M + bm - 1) / bm;
+  const int bm = 64 * HYB_MB, tiles_n = n_rows / 64, full = (M + bm - 1) / bm;
   double best = list_makespan(full * tiles_n, 0, 1.0, cus);
   for (int j = full - 1; j >= 0; j--) {
     const int tail = (M - j * bm + 63) / 64 * tiles_n;
@@ -814,7 +871,7 @@ GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus) {
 hipError_t launch_gemm_hybrid(int epi, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (pl.bn != 64 || pl.mw != 4 || a.K % 256 || !a.A || !a.d8 || !a.bsop) return hipErrorInvalidValue;
-  if (pl.tail_mb && (pl.tail_mb != 1 || pl.m_main < 0 || pl.m_main % 128 || pl.m_main >= a.M))
+  if (pl.tail_mb && (pl.tail_mb != 1 || pl.m_main < 0 || pl.m_main % (64 * HYB_MB) || pl.m_main >= a.M))
     return hipErrorInvalidValue;
   if (epi == EPI_GATED) {
     if (a.N % 32 || !a.W1) return hipErrorInvalidValue;
