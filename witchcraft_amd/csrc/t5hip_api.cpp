@@ -488,11 +488,18 @@ struct NormLink {
 };
 
 // True when this forward's GEMMs fold the norms (the row fits one norm record).
-bool fold_norm(const t5h_model* m, int T) {
+// The block's first T5LayerNorm (before QKV) is folded into the GEMM that produces its input
+// (the embedding gather, the previous block's wo) and into the QKV GEMM.
+bool fold_attn_norm(const t5h_model* m, int T) {
   (void)T;
   const int D = m->cfg.d_model;
-  // the hybrid FFN and projection normalise their own f32 input, so no norm is folded there
-  return !m->fold_norm_off && m->numerics == T5H_NUMERICS_DEFAULT && D % 64 == 0 && D <= NORM_REC_MAX_D;
+  return !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
+}
+
+// Every norm folded.  With hybrid numerics the FFN's and the projection's Q8_K quantizer
+// normalises its own f32 input, so only the attention norm is folded there.
+bool fold_norm(const t5h_model* m, int T) {
+  return fold_attn_norm(m, T) && m->numerics == T5H_NUMERICS_DEFAULT;
 }
 
 // Hybrid numerics (t5h_set_numerics): the FFN's gate|up and the projection quantize their f32
@@ -761,31 +768,45 @@ const float* prenorm(t5h_model* m, const float* w, int T, int& rc) {
 }
 
 // T5LayerNorm of the residual stream in record mode, for GEMMs that fold the norm.
-int prenorm_rec(t5h_model* m, const float* w, int T) {
+int prenorm_rec(t5h_model* m, const float* w, int T, float* rec) {
   Timed t(m, K_RMSNORM, 0, (double)T * m->cfg.d_model * 6);
   const hipError_t e = t5k::launch_rmsnorm(m->w.x, w, m->w.xn, T, m->cfg.d_model, m->cfg.layer_norm_epsilon,
-                                           m->stream, m->w.rec0, rec_stride(m, T));
+                                           m->stream, rec, rec_stride(m, T));
   if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("rmsnorm launch: ") + hipGetErrorString(e));
-  record_rmsnorm(m, w, T, m->w.rec0, rec_stride(m, T));
+  record_rmsnorm(m, w, T, rec, rec_stride(m, T));
   return T5H_OK;
 }
 
 // One encoder block.  When the GEMMs fold the norms (fold_norm), the operand of the
 // block's first norm is either made here (operand_ready false) or was left in m->w.xn / rec0 by
 // the previous block's wo GEMM; with next_gamma set, this block's wo GEMM in turn prepares the
-// operand of the norm that follows (next block's first norm or the final one).
+// operand of the norm that follows (next block's first norm or the final one).  With hybrid
+// numerics only the first norm is folded (fold_attn_norm): QKV passes its operand scale on to
+// wo, whose records the next block's QKV reads, so the two record buffers swap roles from one
+// block to the next (even blocks read rec0).
 int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
               const float* next_gamma = nullptr) {
   const t5h_config& c = m->cfg;
   const Layer& Ly = m->layers[l];
   const int D = c.d_model, inner = m->inner;
-  const bool fold = fold_norm(m, T);
+  const bool hybrid = m->numerics == T5H_NUMERICS_HYBRID;
+  const bool fold = fold_norm(m, T), fold0 = fold_attn_norm(m, T);
   int rc;
   const float* nw0 = nullptr;
   NormLink qn, on, fn, wn;  // QKV consumer, O producer, FFN consumer, wo producer
   const NormLink* qkv_nl = nullptr;
-  if (fold) {
-    if (!operand_ready && (rc = prenorm_rec(m, Ly.ln0, T))) return rc;
+  if (hybrid && fold0) {
+    float* ra = (l & 1) ? m->w.rec1 : m->w.rec0;
+    float* rb = (l & 1) ? m->w.rec0 : m->w.rec1;
+    if (!operand_ready && (rc = prenorm_rec(m, Ly.ln0, T, ra))) return rc;
+    qn.rec = ra;
+    qn.rec_next = rb;
+    wn.rec = rb;
+    wn.nx = m->w.xn;
+    wn.ngamma = next_gamma;
+    qkv_nl = &qn;
+  } else if (fold) {
+    if (!operand_ready && (rc = prenorm_rec(m, Ly.ln0, T, m->w.rec0))) return rc;
     qn.rec = m->w.rec0;
     qn.rec_next = m->w.rec1;
     on.rec = m->w.rec1;
@@ -832,9 +853,10 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
   if ((rc = gemm(m, K_GEMM_O, EPI_RESID, Ly.o, nullptr, m->w.ao, inner, T, m->w.x, D, 0, nullptr, fold ? &on : nullptr)))
     return rc;
   const float* nw1 = nullptr;
-  if (m->numerics == T5H_NUMERICS_HYBRID) {
+  if (hybrid) {
     if ((rc = hybrid_linear(m, K_GEMM_GATE_UP, Ly.ln1, Ly.wi0, &Ly.wi1, T, nullptr, 0))) return rc;
-    return gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, D, 0, nullptr, nullptr);
+    return gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->w.hb, c.d_ff, T, m->w.x, D, 0, nullptr,
+                fold0 && next_gamma ? &wn : nullptr);
   }
   if (!fold) {
     nw1 = prenorm(m, Ly.ln1, T, rc);
@@ -872,8 +894,11 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
                   int normalize) {
   int rc;
   const t5h_config& c = m->cfg;
-  // With folded norms the embedding gather also emits the first norm's operand and records.
-  const bool fold = fold_norm(m, T);
+  // With folded norms the embedding gather also emits the first norm's operand and records
+  // (hybrid numerics: when there is a block, whose QKV folds it; the projection's quantizer
+  // normalises its own input).
+  const bool hybrid = m->numerics == T5H_NUMERICS_HYBRID;
+  const bool fold = fold_norm(m, T) || (fold_attn_norm(m, T) && c.num_layers > 0);
   {
     // algorithmic bytes: the table rows read (f32, or 144 B per 256 values of a Q4_K table), x
     // written (f32), and with the folded norm the f16 operand and the 64-byte record per token
@@ -902,7 +927,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
     }
   }
   for (int l = 0; l < c.num_layers; l++) {
-    const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : m->final_ln;
+    const float* next = l + 1 < c.num_layers ? m->layers[l + 1].ln0 : (hybrid ? nullptr : m->final_ln);
     if ((rc = run_block(m, l, T, nwork, fold, next))) return rc;
   }
   const float* nwf = nullptr;
