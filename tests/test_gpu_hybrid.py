@@ -259,3 +259,21 @@ def test_q4k_q8k_matmul_single_token(enc):
     wd = orc.q4k_dequant(w).reshape(N, K).astype(np.float64)
     scale = np.abs(_q8k_dequant(x8[0]))[None, :] @ np.abs(wd).T
     assert np.all(np.abs(got - want) <= 1e-6 * scale + 1e-30)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [193, 200, 450])
+def test_q4k_q8k_matmul_tile_padding(enc, T):
+    """Token counts whose last full tile reaches past roundup(T, 256): the buffers are padded to
+    the hybrid tile height, and every row matches the oracle's vec_dot."""
+    rng = np.random.default_rng(76 + T)
+    K, N = 512, 128
+    w = quantize_q4k((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x8 = enc.q8k_quantize(rng.standard_normal((T, K)).astype(np.float32))
+    got = enc.q4k_q8k_matmul(w, x8, K)
+    assert got.shape == (T, N) and np.isfinite(got).all()
+    for t in (0, T // 2, T - 1):
+        want = np.array([orc.q4k_q8k_vec_dot(K, w[n], x8[t]) for n in range(N)], np.float32)
+        wd = orc.q4k_dequant(w).reshape(N, K).astype(np.float64)
+        scale = np.abs(_q8k_dequant(x8[t])) @ np.abs(wd).T
+        assert np.all(np.abs(got[t] - want) <= 1e-6 * scale + 1e-30)

@@ -501,15 +501,18 @@ def test_sequence_output_independent_of_batch_neighbours(xtr):
 
 def _handles_by_tail(enc_mod, img, cfg):
     """Handles on one model with the batched GEMM's thin tail tiles off (T5H_GEMM_TAIL=0),
-    forced to 16 (1) and to 32 (2) token rows per math wave for the last row of full tiles."""
+    forced to 16 (1) and to 32 (2) token rows per math wave for the last row of full tiles, and
+    with full tiles of 48 tokens per math wave and thin tails of 32 (T5H_GEMM_MB=3, "mb3")."""
     import os
     hs = {}
-    for v in ("0", "1", "2"):
-        os.environ["T5H_GEMM_TAIL"] = v
+    for v in ("0", "1", "2", "mb3"):
+        env = {"T5H_GEMM_TAIL": "2", "T5H_GEMM_MB": "3"} if v == "mb3" else {"T5H_GEMM_TAIL": v}
+        os.environ.update(env)
         try:
             hs[v] = enc_mod.T5EncoderModel.from_gguf(img, cfg)
         finally:
-            del os.environ["T5H_GEMM_TAIL"]
+            for k in env:
+                del os.environ[k]
     return hs
 
 
@@ -530,7 +533,7 @@ def test_thin_tail_tiles_are_bit_identical(enc_mod, xtr, layout):
             assert cu[-1] % 256, "the batch must end in a partial row of tiles"
             ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
             ref, _ = hs["0"].encode_packed(ids, cu)
-            for v in ("1", "2"):
+            for v in ("1", "2", "mb3"):
                 got, _ = hs[v].encode_packed(ids, cu)
                 assert np.array_equal(got, ref), (layout, int(cu[-1]), v)
             auto, _ = gpu.encode_packed(ids, cu)

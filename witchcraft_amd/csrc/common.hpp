@@ -174,10 +174,12 @@ hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipSt
 // Tile plan of one batched GEMM launch: full tiles of 64*mw token rows x bn weight rows
 // cover rows [0, m_main); thin tiles of 16*tail_mb rows per math wave cover [m_main, M)
 // (tail_mb = 0: full tiles everywhere).
+// mb: 16-token row blocks per math wave in the full tiles (4, or 3 with mw = 4).
 struct GemmPlan {
-  int mw = 4, bn = 128, m_main = 0, tail_mb = 0;
+  int mw = 4, bn = 128, m_main = 0, tail_mb = 0, mb = 4;
 };
-GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override);
+GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override,
+                   int mb_override = 0);
 hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& plan, const GemmArgs& a, hipStream_t s);
 // Small-M variant (M <= GEMV_MAX_M tokens), same arguments and results.
 constexpr int GEMV_MAX_M = 64;
@@ -231,5 +233,8 @@ hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, int8_t* xq, 
 // (8 hi + lo); the block then adds d4 d8 * sum - dmin4 d8 * (mins . bsums) in f32.  epi:
 // EPI_GATED (gelu_pade(W0) * W1 into the f16 operand, operand order) or EPI_F32.  Q4_K weights, bn = 64, K <= 1024.
 GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus);
+// Rows of the A operand, d8 and bsop a hybrid launch over M tokens may read (its full tiles
+// round M up to the tile height): the buffers must hold at least this many.
+int gemm_hybrid_rows(int M);
 hipError_t launch_gemm_hybrid(int epi, const GemmPlan& plan, const GemmArgs& a, hipStream_t s);
 }  // namespace t5k

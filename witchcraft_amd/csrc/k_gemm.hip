@@ -241,7 +241,7 @@ __device__ __forceinline__ void qkv_store_staged(const GemmArgs& p, int mrow0, i
 template <int BN, int MB>
 __device__ __forceinline__ void resid_store_tile(const GemmArgs& p, int mrow0, int n0, const f4 (&acc)[MB][BN / 16]) {
   constexpr int NB = BN / 16, G = BN / 64;
-  constexpr int CH = BN == 64 ? MB : (MB >= 2 ? 2 : 1);  // row blocks whose x is read at once
+  constexpr int CH = BN == 64 ? MB : (MB % 2 == 0 ? 2 : 1);  // row blocks whose x is read at once
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   const bool fold = p.nx != nullptr;
   float* x = (float*)p.out;
@@ -682,7 +682,7 @@ struct GemmGrid {
   int tiles_n, main_tiles, main_blocks, m_main, tail_tiles;
 };
 
-template <int EPI, int WF, int MW, int BN, int S, int TMB, bool HY = false>
+template <int EPI, int WF, int MW, int BN, int S, int TMB, bool HY = false, int FMB = 4>
 __global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_kernel(GemmArgs p, GemmGrid g) {
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
@@ -692,9 +692,9 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
   // hybrid numerics: the math waves' block sums for the fold waves
   __shared__ int4 Sx[HY ? MW * HYB_MB * (BN / 16) * 64 : 1];
   constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN;  // output columns per tile
-  // Full tiles: 4 row blocks per math wave; HYB_MB with hybrid numerics, whose math waves hold
-  // two int32 accumulator sets (the planes' block sums).
-  constexpr int MBM = HY ? HYB_MB : 4;
+  // Full tiles: FMB (4 or 3) row blocks per math wave; HYB_MB with hybrid numerics, whose math
+  // waves hold two int32 accumulator sets (the planes' block sums).
+  constexpr int MBM = HY ? HYB_MB : FMB;
   int b = blockIdx.x;
   if (TMB == 0 || b < g.main_blocks) {
     const int tile = (b % 8) * (g.main_blocks / 8) + b / 8;
@@ -703,7 +703,7 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
       gemm_tile<EPI, WF, MW, BN, S, MBM, true>(p, (tile / g.tiles_n) * 16 * MBM * MW, (tile % g.tiles_n) * cols, Bs,
                                                Md, Mm, Sx);
     else
-      gemm_tile<EPI, WF, MW, BN, S, 4>(p, (tile / g.tiles_n) * 64 * MW, (tile % g.tiles_n) * cols, Bs);
+      gemm_tile<EPI, WF, MW, BN, S, MBM>(p, (tile / g.tiles_n) * 16 * MBM * MW, (tile % g.tiles_n) * cols, Bs);
   } else {
     constexpr int MBT = TMB == 0 ? 1 : TMB;
     b -= g.main_blocks;
@@ -718,9 +718,9 @@ void gemm_kernel(GemmArgs p, GemmGrid g) {
   }
 }
 
-template <int EPI, int WF, int BN, int S, int MW, int TMB, bool HY = false>
+template <int EPI, int WF, int BN, int S, int MW, int TMB, bool HY = false, int FMB = 4>
 hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
-  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = (HY ? 16 * HYB_MB : 64) * MW;
+  constexpr int cols = EPI == EPI_GATED ? BN / 2 : BN, bm = 16 * (HY ? HYB_MB : FMB) * MW;
   GemmGrid g;
   g.tiles_n = a.N / cols;
   g.m_main = TMB ? pl.m_main : a.M;
@@ -730,7 +730,7 @@ hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s
   g.tail_tiles = TMB ? (a.M - g.m_main + bmt - 1) / bmt * g.tiles_n : 0;
   const int grid = g.main_blocks + (g.tail_tiles + 7) / 8 * 8;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB, HY>), dim3(grid), dim3(128 * MW), 0, s, a, g);
+  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB, HY, FMB>), dim3(grid), dim3(128 * MW), 0, s, a, g);
   return hipGetLastError();
 }
 
@@ -739,6 +739,11 @@ hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s
 template <int EPI, int WF, int BN>
 hipError_t launch_cfg(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (pl.mw == 2) return launch_plan<EPI, WF, BN, 2, 2, 0>(pl, a, s);
+  if (pl.mb == 3) switch (pl.tail_mb) {
+      case 1: return launch_plan<EPI, WF, BN, 2, 4, 1, false, 3>(pl, a, s);
+      case 2: return launch_plan<EPI, WF, BN, 2, 4, 2, false, 3>(pl, a, s);
+      default: return launch_plan<EPI, WF, BN, 2, 4, 0, false, 3>(pl, a, s);
+    }
   switch (pl.tail_mb) {
     case 1: return launch_plan<EPI, WF, BN, 2, 4, 1>(pl, a, s);
     case 2: return launch_plan<EPI, WF, BN, 2, 4, 2>(pl, a, s);
@@ -815,39 +820,62 @@ static double thin_tile_cost(int bn, int mb) {
 // Full tiles for rows [0, m_main), thin tiles for the rest, where that shortens the launch:
 // with one workgroup per CU a launch of T full tiles takes ceil(T / CUs) rounds, and a last
 // round that is mostly empty costs as much as a full one.  Every split at a multiple of the
-// full tile height and both thin heights is evaluated with list_makespan.
+// full tile height and both thin heights is evaluated with list_makespan, for full tiles of 64
+// and of 48 tokens per math wave: the shorter tile costs 0.82 of the longer one (cfg4's M =
+// 70,983, where rounds do not quantize: gate|up 561 vs 612 us, QKV 316 vs 343 us for 4/3 as
+// many tiles) and wins where it fills the last round better (cfg2 gate|up 36.9 -> 33.7 us, QKV
+// 23.5 -> 22.4 us; O and wo stay on one round of 64-token tiles).
 // tail_override: -1 = choose, 0 = full tiles only, 1 / 2 = thin tiles of that height for the
-// last row of full tiles, 3 / 4 = thin tiles of height 1 / 2 for every row (tests, tuning).
-GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override) {
+// last row of full tiles, 3 / 4 = thin tiles of height 1 / 2 for every row (tests, tuning); a
+// tail override keeps 64-token full tiles unless mb_override (3 or 4) sets their height.
+static double full_tile_cost(int mb) { return mb == 3 ? 0.82 : 1.0; }
+
+GemmPlan gemm_plan(int M, int n_rows, int cus, int mw_override, int bn_override, int tail_override,
+                   int mb_override) {
   GemmPlan pl;
   gemm_pick_tile(M, n_rows, cus, pl.mw, pl.bn);
   if (mw_override == 2 || mw_override == 4) pl.mw = mw_override;
   if (bn_override == 64 || bn_override == 128) pl.bn = bn_override;
+  pl.mb = pl.mw == 4 && mb_override == 3 ? 3 : 4;
   pl.m_main = M;
   pl.tail_mb = 0;
-  if (pl.mw != 4 || M <= 0 || tail_override == 0) return pl;
-  const int bm = 256, tiles_n = n_rows / pl.bn, full = (M + bm - 1) / bm;
-  if (tail_override >= 1 && tail_override <= 4) {  // 3, 4: every row in thin tiles of height 1, 2
-    pl.tail_mb = tail_override > 2 ? tail_override - 2 : tail_override;
-    pl.m_main = tail_override > 2 ? 0 : (full - 1) * bm;
+  if (pl.mw != 4 || M <= 0) return pl;
+  const int tiles_n = n_rows / pl.bn;
+  if (tail_override >= 0) {
+    const int bm = 64 * pl.mb, full = (M + bm - 1) / bm;
+    if (tail_override >= 1 && tail_override <= 4) {  // 3, 4: every row in thin tiles of height 1, 2
+      pl.tail_mb = tail_override > 2 ? tail_override - 2 : tail_override;
+      pl.m_main = tail_override > 2 ? 0 : (full - 1) * bm;
+    }
     return pl;
   }
-  double best = list_makespan(full * tiles_n, 0, 1.0, cus);
-  for (int j = full - 1; j >= 0; j--)
-    for (int mb = 1; mb <= 2; mb++) {
-      const int bmt = 64 * mb, tail = (M - j * bm + bmt - 1) / bmt * tiles_n;
-      const double t = list_makespan(j * tiles_n, tail, thin_tile_cost(pl.bn, mb), cus);
+  double best = 1e30;
+  for (int mb = 4; mb >= 3; mb--) {
+    if (mb_override && mb != pl.mb) continue;
+    const int bm = 64 * mb, full = (M + bm - 1) / bm;
+    const double cf = full_tile_cost(mb);
+    auto consider = [&](double t, int m_main, int tail_mb) {
       if (t < best - 1e-9) {
         best = t;
-        pl.m_main = j * bm;
-        pl.tail_mb = mb;
+        pl.mb = mb;
+        pl.m_main = m_main;
+        pl.tail_mb = tail_mb;
       }
-    }
+    };
+    consider(list_makespan(full * tiles_n, 0, 1.0, cus) * cf, M, 0);
+    for (int j = full - 1; j >= 0; j--)
+      for (int tmb = 1; tmb <= 2; tmb++) {
+        const int bmt = 64 * tmb, tail = (M - j * bm + bmt - 1) / bmt * tiles_n;
+        consider(list_makespan(j * tiles_n, tail, thin_tile_cost(pl.bn, tmb) / cf, cus) * cf, j * bm, tmb);
+      }
+  }
   return pl;
 }
 
 // Hybrid plans: full tiles of 32 mw tokens (two row blocks per math wave) x 64 weight rows, or
 // with tail_mb = 1 thin tiles of one row block per math wave for rows [m_main, M).
+int gemm_hybrid_rows(int M) { return (M + 64 * HYB_MB - 1) / (64 * HYB_MB) * (64 * HYB_MB); }
+
 GemmPlan gemm_plan_hybrid(int M, int n_rows, int cus) {
   GemmPlan pl;
   pl.bn = 64;
@@ -886,7 +914,8 @@ hipError_t launch_gemm_hybrid(int epi, const GemmPlan& pl, const GemmArgs& a, hi
 hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (pl.mw != 2 && pl.mw != 4) return hipErrorInvalidValue;
-  if (pl.tail_mb && (pl.mw != 4 || pl.m_main < 0 || pl.m_main % 256 || pl.m_main >= a.M))
+  if (pl.mb != 4 && !(pl.mb == 3 && pl.mw == 4)) return hipErrorInvalidValue;
+  if (pl.tail_mb && (pl.mw != 4 || pl.m_main < 0 || pl.m_main % (64 * pl.mb) || pl.m_main >= a.M))
     return hipErrorInvalidValue;
   if (pl.bn != 64 && pl.bn != 128) return hipErrorInvalidValue;
   // whole tiles along N and whole 4-step rings of 64-wide K steps

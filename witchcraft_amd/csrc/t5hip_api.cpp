@@ -171,6 +171,7 @@ struct t5h_model {
   int gemm_mw_override = 0;  // T5H_GEMM_MW / T5H_GEMM_BN tuning knobs (0 = heuristic)
   bool batched_only = false;  // route every linear through the batched GEMM (t5h_ffn_block mode 1)
   int gemm_bn_override = 0;
+  int gemm_mb_override = 0;  // T5H_GEMM_MB: 3 / 4 row blocks per math wave in full tiles (0 = choose)
   int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail, 3 / 4 = all thin
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
   int numerics = T5H_NUMERICS_DEFAULT;  // t5h_set_numerics
@@ -512,6 +513,8 @@ int hybrid_linear(t5h_model* m, int kind, const float* ln, const Linear& W0, con
                   int ldo) {
   const t5h_config& c = m->cfg;
   const int nblk = c.d_model / QK_K;
+  if (t5k::gemm_hybrid_rows(T) > m->w.tpad)  // roundup(T, 512) + 128 covers every tile height used
+    return fail(T5H_ERR_INVALID, "internal: hybrid GEMM tiles exceed the workspace rows");
   float* d8 = (float*)m->w.ao;
   _Float16* bs = (_Float16*)((uint8_t*)m->w.ao + align256((size_t)m->w.tpad * nblk * 4));
   Timed t(m, kind, 2.0 * T * W0.N * W0.K * (W1 ? 2 : 1), 0);
@@ -604,7 +607,7 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
   const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
-                                            m->gemm_bn_override, m->gemm_tail_override);
+                                            m->gemm_bn_override, m->gemm_tail_override, m->gemm_mb_override);
   HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
   if (m->prof) {
     ReplayRec& r = m->replay[kind];
@@ -1201,6 +1204,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     const int v = atoi(e);
     if (v == 64 || v == 128) m->gemm_bn_override = v;
   }
+  if (const char* e = getenv("T5H_GEMM_MB")) {
+    const int v = atoi(e);
+    if (v == 3 || v == 4) m->gemm_mb_override = v;
+  }
   if (const char* e = getenv("T5H_GEMM_TAIL")) {
     const int v = atoi(e);
     if (v >= 0 && v <= 4) m->gemm_tail_override = v;
@@ -1614,7 +1621,7 @@ int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const ui
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, hip_device);
   // the GEMM's tiles read operand rows up to a whole tile past T
-  const int tpad = (T + 255) / 256 * 256, nblk = K / QK_K;
+  const int tpad = t5k::gemm_hybrid_rows(T), nblk = K / QK_K;
   const size_t wb = (size_t)N * K / QK_K * Q4K_BYTES, x8b = (size_t)T * t5k::q8k_bytes_per_row(K),
                xqb = (size_t)tpad * K, d8b = (size_t)tpad * nblk * 4, bsb = (size_t)tpad * nblk * 64,
                ob = (size_t)T * N * 4;
