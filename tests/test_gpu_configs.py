@@ -130,6 +130,46 @@ def test_cfg4_bench_batch_vs_oracle(xtr, cfg4_run):
     _vs_oracle(ora, ids, cu, out, _sample(cu, 16, 11), "cfg4")
 
 
+def test_cfg4_two_lanes_bit_identical(xtr, cfg4_run):
+    """Batches of >= 24576 tokens run as two halves on two streams: the same bits as one lane
+    (T5H_SPLIT=0), through the host and the device entry points, and the hybrid numerics too."""
+    import os
+    import torch
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, gpu, _ = xtr
+    ids, cu, out, norms = cfg4_run
+    os.environ["T5H_SPLIT"] = "0"
+    try:
+        one = T5EncoderModel.from_gguf(img, cfg)
+    finally:
+        del os.environ["T5H_SPLIT"]
+    try:
+        ref, ref_n = one.encode_packed(ids, cu)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(norms.view(np.uint32), ref_n.view(np.uint32))
+        dev = torch.device("cuda:0")
+        d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+        d_out = torch.empty((int(cu[-1]), cfg["proj_dim"]), dtype=torch.float32, device=dev)
+        d_norm = torch.empty(int(cu[-1]), dtype=torch.float32, device=dev)
+        for _ in range(2):  # the second call reuses both lanes' work lists
+            d_out.zero_()
+            gpu.encode_device(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+            gpu.synchronize()
+            assert np.array_equal(d_out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+            assert np.array_equal(d_norm.cpu().numpy().view(np.uint32), ref_n.view(np.uint32))
+        for h in (gpu, one):
+            h.set_numerics(1)
+        try:
+            a, _ = gpu.encode_packed(ids, cu)
+            b, _ = one.encode_packed(ids, cu)
+            assert np.isfinite(a).all() and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        finally:
+            for h in (gpu, one):
+                h.set_numerics(0)
+    finally:
+        one.close()
+
+
 def test_cfg5_bench_batch_properties(xtr_hybrid, cfg5_run):
     _, _, gpu, _ = xtr_hybrid
     ids, cu, out, _ = cfg5_run
