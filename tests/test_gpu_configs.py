@@ -131,7 +131,7 @@ def test_cfg4_bench_batch_vs_oracle(xtr, cfg4_run):
 
 
 def test_cfg4_two_lanes_bit_identical(xtr, cfg4_run):
-    """Batches of >= 24576 tokens run as two halves on two streams: the same bits as one lane
+    """Batches of >= 16384 tokens run as two halves on two streams: the same bits as one lane
     (T5H_SPLIT=0), through the host and the device entry points, and the hybrid numerics too."""
     import os
     import torch

@@ -241,6 +241,7 @@ struct t5h_model {
 
   // ---- second lane for large batches (enqueue_forward) ----
   bool split_off = false;  // T5H_SPLIT=0: one lane for every batch
+  int split_min = 0;       // T5H_SPLIT=<tokens> (> 1): two lanes from that many tokens (0: SPLIT_MIN_TOKENS)
   ExecLane lane1;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 
@@ -944,14 +945,16 @@ void swap_lane(t5h_model* m) {
 
 // Batches of at least this many tokens (and two or more sequences) run as two halves, split at
 // the sequence boundary nearest T / 2, on two streams: one half's launches fill the CUs the
-// other's leave idle (tails of GEMM rounds, attention).  Measured at cfg4 (71 k tokens): 18.7 vs
-// 17.7 ms per step, bit-identical outputs (every output row is computed the same way: the
-// GEMMs keep one K order per output at any tile plan, attention is per sequence).
-constexpr int SPLIT_MIN_TOKENS = 24576;
+// other's leave idle (tails of GEMM rounds, attention).  Measured per step, one lane vs two:
+// 71 k tokens (cfg4) 18.7 vs 17.5 ms, 16.8 k (cfg5) 4.29 vs 4.22 ms and 5.57 vs 5.35 ms with
+// hybrid numerics; 9.2 k and 4.4 k tokens are slower on two (2.48 vs 2.58 ms, 1.38 vs 1.42 ms).
+// Outputs are bit-identical (every output row is computed the same way: the GEMMs keep one K
+// order per output at any tile plan, attention is per sequence).
+constexpr int SPLIT_MIN_TOKENS = 16384;
 
 int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
                     float* d_norm, int normalize) {
-  if (m->split_off || m->prof || B < 2 || T < SPLIT_MIN_TOKENS)
+  if (m->split_off || m->prof || B < 2 || T < (m->split_min > 0 ? m->split_min : SPLIT_MIN_TOKENS))
     return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
   int s = 1;
   for (int b = 2; b < B; b++)
@@ -1303,7 +1306,11 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     if (v >= 0 && v <= 4) m->gemm_tail_override = v;
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
-  if (const char* e = getenv("T5H_SPLIT")) m->split_off = atoi(e) == 0;
+  if (const char* e = getenv("T5H_SPLIT")) {
+    const int v = atoi(e);
+    m->split_off = v == 0;
+    if (v > 1) m->split_min = v;
+  }
   const int D = cfg->d_model, F = cfg->d_ff, inner = m->inner, H = cfg->num_heads;
 
   HostArena ha;
