@@ -170,6 +170,34 @@ def test_cfg4_two_lanes_bit_identical(xtr, cfg4_run):
         one.close()
 
 
+def test_two_lanes_with_empty_sequences(xtr):
+    """The two-lane cut with empty sequences: at the front or the end of the batch (a half would
+    hold no tokens, so one lane runs) and inside the second half; same bits as one lane."""
+    import os
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, _, _ = xtr
+    hs = {}
+    for v in ("256", "0"):
+        os.environ["T5H_SPLIT"] = v
+        try:
+            hs[v] = T5EncoderModel.from_gguf(img, cfg)
+        finally:
+            del os.environ["T5H_SPLIT"]
+    try:
+        rng = np.random.default_rng(91)
+        for cu in ([0, 0, 500], [0, 500, 500], [0, 0, 300, 300, 700], [0, 200, 200, 450, 451]):
+            cu = np.array(cu, np.int32)
+            ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+            a, an = hs["256"].encode_packed(ids, cu)
+            b, bn = hs["0"].encode_packed(ids, cu)
+            assert np.isfinite(a).all(), cu
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), cu
+            assert np.array_equal(an.view(np.uint32), bn.view(np.uint32)), cu
+    finally:
+        for h in hs.values():
+            h.close()
+
+
 def test_cfg5_bench_batch_properties(xtr_hybrid, cfg5_run):
     _, _, gpu, _ = xtr_hybrid
     ids, cu, out, _ = cfg5_run

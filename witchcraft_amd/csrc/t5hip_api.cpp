@@ -960,6 +960,8 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
   for (int b = 2; b < B; b++)
     if (std::abs(2 * cu[b] - T) < std::abs(2 * cu[s] - T)) s = b;
   const int TA = cu[s], P = m->cfg.proj_dim;
+  if (TA <= 0 || TA >= T)  // empty sequences at the cut: one half would hold no tokens
+    return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
   if (!m->lane1.stream) {
     HIP_OK(hipStreamCreateWithFlags(&m->lane1.stream, hipStreamNonBlocking));
     HIP_OK(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
