@@ -154,9 +154,9 @@ struct StagingSlot {
   bool used = false;
 };
 
-// A second execution lane of a handle: its own stream, workspace, attention work-list cache and
-// staging slots.  enqueue_forward runs the second half of a large batch on it (swap_lane puts
-// these fields in place of the handle's own for the duration of that half).
+// A further execution lane of a handle: its own stream, workspace, attention work-list cache and
+// staging slots.  enqueue_forward runs a part of a large batch on it (swap_lane puts these
+// fields in place of the handle's own for the duration of that part).
 struct ExecLane {
   hipStream_t stream = nullptr;
   void* ws = nullptr;
@@ -239,24 +239,29 @@ struct t5h_model {
   t5h_kernel_stat stats[K_COUNT]{};
   ReplayRec replay[K_COUNT];
 
-  // ---- second lane for large batches (enqueue_forward) ----
+  // ---- further lanes for large batches (enqueue_forward) ----
+  static constexpr int MAX_LANES = 4;
   bool split_off = false;  // T5H_SPLIT=0: one lane for every batch
-  int split_min = 0;       // T5H_SPLIT=<tokens> (> 1): two lanes from that many tokens (0: SPLIT_MIN_TOKENS)
-  ExecLane lane1;
-  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  int split_min = 0;       // T5H_SPLIT=<tokens> (> 1): lanes from that many tokens (0: SPLIT_MIN_TOKENS)
+  int lanes = 2;           // T5H_LANES: lanes of a large batch (2..MAX_LANES)
+  ExecLane extra[MAX_LANES - 1];
+  hipEvent_t ev_fork = nullptr, ev_join[MAX_LANES - 1] = {};
 
   ~t5h_model() {
-    if (lane1.stream) {
-      (void)hipStreamSynchronize(lane1.stream);
-      (void)hipStreamDestroy(lane1.stream);
+    for (auto& l : extra) {
+      if (l.stream) {
+        (void)hipStreamSynchronize(l.stream);
+        (void)hipStreamDestroy(l.stream);
+      }
+      for (auto& s : l.slots) {
+        if (s.host) (void)hipHostFree(s.host);
+        if (s.done) (void)hipEventDestroy(s.done);
+      }
+      if (l.ws) (void)hipFree(l.ws);
     }
-    for (auto& s : lane1.slots) {
-      if (s.host) (void)hipHostFree(s.host);
-      if (s.done) (void)hipEventDestroy(s.done);
-    }
-    if (lane1.ws) (void)hipFree(lane1.ws);
     if (ev_fork) (void)hipEventDestroy(ev_fork);
-    if (ev_join) (void)hipEventDestroy(ev_join);
+    for (auto e : ev_join)
+      if (e) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamSynchronize(stream);
     for (auto& s : slots) {
       if (s.host) (void)hipHostFree(s.host);
@@ -925,8 +930,7 @@ int enqueue_lane(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, 
   return enqueue_stack(m, d_ids, T, nwork, d_out, d_norm, normalize);
 }
 
-void swap_lane(t5h_model* m) {
-  ExecLane& l = m->lane1;
+void swap_lane(t5h_model* m, ExecLane& l) {
   std::swap(m->stream, l.stream);
   std::swap(m->ws, l.ws);
   std::swap(m->ws_bytes, l.ws_bytes);
@@ -954,35 +958,51 @@ constexpr int SPLIT_MIN_TOKENS = 16384;
 
 int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, int T, float* d_out,
                     float* d_norm, int normalize) {
-  if (m->split_off || m->prof || B < 2 || T < (m->split_min > 0 ? m->split_min : SPLIT_MIN_TOKENS))
+  const int tmin = m->split_min > 0 ? m->split_min : SPLIT_MIN_TOKENS;
+  if (m->split_off || m->prof || B < 2 || T < tmin)
     return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
-  int s = 1;
-  for (int b = 2; b < B; b++)
-    if (std::abs(2 * cu[b] - T) < std::abs(2 * cu[s] - T)) s = b;
-  const int TA = cu[s], P = m->cfg.proj_dim;
-  if (TA <= 0 || TA >= T)  // empty sequences at the cut: one half would hold no tokens
-    return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
-  if (!m->lane1.stream) {
-    HIP_OK(hipStreamCreateWithFlags(&m->lane1.stream, hipStreamNonBlocking));
-    HIP_OK(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
-    HIP_OK(hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming));
+  // parts: cut at the sequence boundaries nearest k T / n; a part without tokens (empty
+  // sequences at a cut) ends the split there
+  const int n = std::min(m->lanes, B);
+  int cut[t5h_model::MAX_LANES + 1];
+  int parts = 1;
+  cut[0] = 0;
+  for (int k = 1; k < n; k++) {
+    int s = cut[parts - 1] + 1;
+    for (int b = s + 1; b < B; b++)
+      if (std::abs(n * cu[b] - k * T) < std::abs(n * cu[s] - k * T)) s = b;
+    if (s >= B || cu[s] <= cu[cut[parts - 1]] || cu[s] >= T) break;
+    cut[parts++] = s;
   }
-  // lane 1 starts after everything enqueued on the handle's stream so far (the inputs)
+  if (parts == 1) return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
+  cut[parts] = B;
+  const int P = m->cfg.proj_dim;
+  if (!m->ev_fork) HIP_OK(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
+  for (int i = 0; i + 1 < parts; i++) {
+    if (!m->extra[i].stream) HIP_OK(hipStreamCreateWithFlags(&m->extra[i].stream, hipStreamNonBlocking));
+    if (!m->ev_join[i]) HIP_OK(hipEventCreateWithFlags(&m->ev_join[i], hipEventDisableTiming));
+  }
+  // the other lanes start after everything enqueued on the handle's stream so far (the inputs)
   HIP_OK(hipEventRecord(m->ev_fork, m->stream));
-  int rc = enqueue_lane(m, d_ids, cu, s, TA, d_out, d_norm, normalize);
+  int rc = enqueue_lane(m, d_ids, cu, cut[1], cu[cut[1]], d_out, d_norm, normalize);
   if (rc) return rc;
-  std::vector<int32_t> cub(B - s + 1);
-  for (int i = 0; i <= B - s; i++) cub[i] = cu[s + i] - TA;
-  HIP_OK(hipStreamWaitEvent(m->lane1.stream, m->ev_fork, 0));
-  swap_lane(m);
-  rc = enqueue_lane(m, d_ids + TA, cub.data(), B - s, T - TA, d_out + (size_t)TA * P, d_norm ? d_norm + TA : nullptr,
-                    normalize);
-  const hipError_t e = rc ? hipSuccess : hipEventRecord(m->ev_join, m->stream);
-  swap_lane(m);
-  if (rc) return rc;
-  HIP_OK(e);
-  // the handle's stream (what callers synchronise or order after) waits for lane 1
-  HIP_OK(hipStreamWaitEvent(m->stream, m->ev_join, 0));
+  std::vector<int32_t> cub;
+  for (int i = 1; i < parts; i++) {
+    const int b0 = cut[i], nb = cut[i + 1] - b0, t0 = cu[b0];
+    cub.assign(cu + b0, cu + b0 + nb + 1);
+    for (auto& c : cub) c -= t0;
+    ExecLane& l = m->extra[i - 1];
+    HIP_OK(hipStreamWaitEvent(l.stream, m->ev_fork, 0));
+    swap_lane(m, l);
+    rc = enqueue_lane(m, d_ids + t0, cub.data(), nb, cub[nb], d_out + (size_t)t0 * P, d_norm ? d_norm + t0 : nullptr,
+                      normalize);
+    const hipError_t e = rc ? hipSuccess : hipEventRecord(m->ev_join[i - 1], m->stream);
+    swap_lane(m, l);
+    if (rc) return rc;
+    HIP_OK(e);
+    // the handle's stream (what callers synchronise or order after) waits for this lane
+    HIP_OK(hipStreamWaitEvent(m->stream, m->ev_join[i - 1], 0));
+  }
   return T5H_OK;
 }
 
@@ -1308,6 +1328,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     if (v >= 0 && v <= 4) m->gemm_tail_override = v;
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
+  if (const char* e = getenv("T5H_LANES")) {
+    const int v = atoi(e);
+    if (v >= 2 && v <= t5h_model::MAX_LANES) m->lanes = v;
+  }
   if (const char* e = getenv("T5H_SPLIT")) {
     const int v = atoi(e);
     m->split_off = v == 0;
