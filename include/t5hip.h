@@ -94,9 +94,12 @@ int t5h_encode_device(t5h_model* model, const uint32_t* d_ids, const int32_t* cu
  * array of T5H_NOALLOC_SCRATCH_BYTES per GPU, mapped by t5h_create and held by every GPU the
  * library runs on until the process ends (about 2,000 tokens of XTR-base per call).  Inputs
  * whose workspace does not fit return T5H_ERR_INVALID before anything is enqueued.  All calls
- * on one GPU share that GPU's array: calls that overlap on one GPU (two handles on two
- * streams, or two threads) race and must be serialised by the caller.  No per-kernel event
- * timing is recorded for these calls. */
+ * on one GPU share that GPU's array, so the library orders them: each call's stream first waits
+ * for a per-GPU event (created by t5h_create) that the previous no-alloc call on that GPU
+ * recorded after its launches, whichever handle or thread made it.  A call enqueued while the
+ * handle's stream is being captured into a graph is not ordered that way (its launches run at
+ * replay time): replays of such graphs must not overlap each other or other no-alloc calls on
+ * the same GPU.  No per-kernel event timing is recorded for these calls. */
 #define T5H_NOALLOC_SCRATCH_BYTES (40u << 20)
 int t5h_encode_device_noalloc(t5h_model* model, const uint32_t* d_ids, const int32_t* cu_seqlens,
                               int32_t B, float* d_out, float* d_norm);
@@ -132,9 +135,16 @@ int t5h_embed_batch(t5h_model* model, const uint32_t* ids, const int32_t* doc_of
  *   (candle BlockQ8K::from_float) times Q4_K weights by GGML's integer vec_dot
  *   (src/fused_matmul.rs:27-59 QTiledOp, :138-177 fused gated gelu with the Pade tanh of
  *   :128-133); the other linears keep the default numerics.  Needs Q4_K wi_0, wi_1 and
- *   linear.weight and a gated FFN.  Default: T5H_NUMERICS_DEFAULT. */
+ *   linear.weight and a gated FFN.  Default: T5H_NUMERICS_DEFAULT.
+ * T5H_NUMERICS_HYBRID_BF16: the `hybrid-dequant` + `fbgemm` build, which `make` selects on
+ *   x86 Linux without nvcc (Makefile:26-30) -- T5H_NUMERICS_HYBRID, with the q/k/v/o/wo weights
+ *   (dequantized to f32 at load, src/quantized_t5.rs:57-62,218-219) truncated to bf16
+ *   (bits & 0xffff0000, fbgemm-rs/src/bf16.rs:21-25) before the f16 MFMAs: exact for |w| >= 2^-17,
+ *   the f16 subnormal grid below.  Q4_K dense weights are expanded on the device on the first
+ *   switch to this mode (2 bytes per weight, kept by the handle). */
 #define T5H_NUMERICS_DEFAULT 0
 #define T5H_NUMERICS_HYBRID 1
+#define T5H_NUMERICS_HYBRID_BF16 2
 int t5h_set_numerics(t5h_model* model, int32_t mode);
 
 /* ---- offline weight quantization (host only, no device needed) ---- */
@@ -279,7 +289,9 @@ int t5h_kernel_stats(t5h_model* model, t5h_kernel_stat* stats, int32_t cap);
  * dispatch and completion latency of every launch; back-to-back relaunches do not, so these
  * averages are comparable with profiler per-dispatch durations.  The relaunches overwrite the
  * workspace (a residual class adds into the residual stream again); the next forward
- * recomputes it. */
+ * recomputes it.  They never touch the profiled call's own buffers (d_ids, d_out, d_norm): the
+ * records use the handle's workspace copies of those instead, so the caller may free them.  A
+ * workspace that grows drops every record (T5H_ERR_INVALID until the next profiled forward). */
 int t5h_replay_kernel(t5h_model* model, int32_t kind, int32_t reps, double* avg_us);
 
 #ifdef __cplusplus

@@ -172,7 +172,8 @@ def test_cfg4_two_lanes_bit_identical(xtr, cfg4_run):
 
 def test_two_lanes_with_empty_sequences(xtr):
     """The two-lane cut with empty sequences: at the front or the end of the batch (a half would
-    hold no tokens, so one lane runs) and inside the second half; same bits as one lane."""
+    hold no tokens, so one lane runs) and inside the second half; and a cut that would leave a
+    part of <= 64 tokens (the GEMV kernels' range: one lane runs); same bits as one lane."""
     import os
     from witchcraft_amd.encoder import T5EncoderModel
     cfg, img, _, _ = xtr
@@ -185,7 +186,8 @@ def test_two_lanes_with_empty_sequences(xtr):
             del os.environ["T5H_SPLIT"]
     try:
         rng = np.random.default_rng(91)
-        for cu in ([0, 0, 500], [0, 500, 500], [0, 0, 300, 300, 700], [0, 200, 200, 450, 451]):
+        for cu in ([0, 0, 500], [0, 500, 500], [0, 0, 300, 300, 700], [0, 200, 200, 450, 451], [0, 500, 530],
+                   [0, 40, 600]):
             cu = np.array(cu, np.int32)
             ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
             a, an = hs["256"].encode_packed(ids, cu)
@@ -209,6 +211,85 @@ def test_cfg5_bench_batch_vs_oracle(xtr_hybrid, cfg5_run):
     _, _, _, ora = xtr_hybrid
     ids, cu, out, _ = cfg5_run
     _vs_oracle(ora, ids, cu, out, _sample(cu, 16, 12), "cfg5")
+
+
+HYBRID_MODES = [(1, orc.VARIANT_HYBRID), (2, orc.VARIANT_HYBRID_BF16)]
+
+
+@pytest.mark.parametrize("mode,variant", HYBRID_MODES, ids=["hybrid", "hybrid_bf16"])
+def test_cfg5_hybrid_numerics_vs_oracle(xtr_hybrid, mode, variant):
+    """The whole cfg5 bench batch (64 sequences, hybrid layout) under each hybrid numerics mode:
+    finite, deterministic, 10 sequences alone bit-identical, and 16 sequences including the
+    longest and the shortest against the oracle's matching variant (hybrid-dequant, and
+    hybrid-dequant + fbgemm with bf16-truncated q/k/v/o/wo: the build `make` picks on x86 Linux,
+    Makefile:26-30)."""
+    cfg, img, gpu, _ = xtr_hybrid
+    ids, cu = synth.ragged_batch(64, 16, 512, cfg["vocab_size"], seed=BATCH_SEED)
+    ora = orc.OracleModel(img, cfg, variant=variant)
+    gpu.set_numerics(mode)
+    try:
+        out, _ = gpu.encode_packed(ids, cu)
+        _properties(gpu, ids, cu, out, f"cfg5 numerics {mode}")
+        _vs_oracle(ora, ids, cu, out, _sample(cu, 16, 13), f"cfg5 numerics {mode}")
+    finally:
+        gpu.set_numerics(0)
+        ora.close()
+
+
+def test_hybrid_bf16_weights_differ_from_hybrid(xtr_hybrid):
+    """The bf16 truncation reaches the GPU: the same batch under the two hybrid modes differs,
+    and each mode is closer to its own oracle variant than to the other one."""
+    cfg, img, gpu, _ = xtr_hybrid
+    ids = np.random.default_rng(95).integers(1, cfg["vocab_size"], size=200).astype(np.uint32)
+    cu = np.array([0, 200], np.int32)
+    outs = {}
+    try:
+        for mode in (1, 2):
+            gpu.set_numerics(mode)
+            outs[mode], _ = gpu.encode_packed(ids, cu)
+    finally:
+        gpu.set_numerics(0)
+    assert not np.array_equal(outs[1], outs[2])
+    refs = {}
+    for mode, variant in HYBRID_MODES:
+        ora = orc.OracleModel(img, cfg, variant=variant)
+        refs[mode] = ora.forward(ids)
+        ora.close()
+    for mode, other in ((1, 2), (2, 1)):
+        assert rel(outs[mode], refs[mode]) < rel(outs[mode], refs[other]), mode
+
+
+@pytest.mark.parametrize("layout,mode,variant",
+                         [("hybrid", 1, orc.VARIANT_HYBRID), ("hybrid", 2, orc.VARIANT_HYBRID_BF16),
+                          ("q4k", 2, orc.VARIANT_HYBRID_BF16)],
+                         ids=["hybrid_layout-hybrid", "hybrid_layout-hybrid_bf16", "q4k_layout-hybrid_bf16"])
+def test_all_layers_teacher_forced_hybrid(xtr, xtr_hybrid, layout, mode, variant):
+    """All 12 XTR-base blocks under the hybrid numerics, each fed the oracle's input for it:
+    relative error <= 1e-3 against the oracle's matching variant over each block's output.  Per
+    token the Q8_K activations can round one step apart where the f16 attention moves a value
+    across a rounding boundary, so the per-token error is only bounded loosely (1e-2)."""
+    cfg, img, gpu, _ = xtr_hybrid if layout == "hybrid" else xtr
+    ora = orc.OracleModel(img, cfg, variant=variant)
+    lens = [96, 130]
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = np.random.default_rng(97 + mode).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    xs = [ora.hidden(ids[cu[b]:cu[b + 1]], 0) for b in range(len(lens))]
+    gpu.set_numerics(mode)
+    worst = 0.0
+    try:
+        for layer in range(cfg["num_layers"]):
+            y = gpu.layer_forward(layer, np.concatenate(xs), cu)
+            xs = [ora.layer(layer, x) for x in xs]
+            y_ref = np.concatenate(xs)
+            per_tok = np.linalg.norm(y - y_ref, axis=1) / np.linalg.norm(y_ref, axis=1)
+            worst = max(worst, float(per_tok.max()))
+            assert rel(y, y_ref) <= LAYER_REL, (layer, rel(y, y_ref))
+            assert per_tok.max() <= 1e-2, (layer, float(per_tok.max()))
+    finally:
+        gpu.set_numerics(0)
+        ora.close()
+    print(f"[layers {layout} numerics {mode}] worst per-token relative error over 12 blocks {worst:.2e}", flush=True)
 
 
 @pytest.mark.parametrize("lens", [[96, 130], [32]], ids=["batched", "gemv"])

@@ -70,3 +70,38 @@ def test_noalloc_rejects_oversized_input(xtr):
     ref, _ = _encode(gpu, False, ids, cu)
     got, _ = _encode(gpu, True, ids, cu)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_noalloc_two_handles_back_to_back(xtr):
+    """Two handles on one GPU share the scratch array.  Calls from both, enqueued back to back on
+    their own streams without any synchronisation between them, must each give the bits of the
+    same calls run one at a time: the library chains the calls through a per-GPU event."""
+    import torch
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, gpu = xtr
+    other = T5EncoderModel.from_gguf(synth.make_model(cfg, seed=0), cfg)
+    try:
+        dev = torch.device("cuda:0")
+        jobs = [(gpu, *_batch(cfg, [400, 300, 211], 11)), (other, *_batch(cfg, [512, 97], 12)),
+                (gpu, *_batch(cfg, [90, 41], 13)), (other, *_batch(cfg, [256, 256, 256], 14))]
+        refs = [_encode(h, False, ids, cu) for h, ids, cu in jobs]
+        bufs = []
+        for h, ids, cu in jobs:
+            T = int(cu[-1])
+            d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+            bufs.append((d_ids, torch.full((T, 128), float("nan"), device=dev), torch.full((T,), float("nan"), device=dev)))
+        torch.cuda.synchronize()
+        for rep in range(3):
+            for (h, ids, cu), (d_ids, d_out, d_norm) in zip(jobs, bufs):
+                h.encode_device_noalloc(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+            for h in (gpu, other):
+                h.synchronize()
+            for k, ((ref, nref), (_, d_out, d_norm)) in enumerate(zip(refs, bufs)):
+                got, ngot = d_out.cpu().numpy(), d_norm.cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rep, k)
+                assert np.array_equal(ngot.view(np.uint32), nref.view(np.uint32)), (rep, k)
+                d_out.fill_(float("nan"))
+                d_norm.fill_(float("nan"))
+            torch.cuda.synchronize()
+    finally:
+        other.close()

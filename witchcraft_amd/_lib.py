@@ -21,6 +21,7 @@ T5H_ERR_NODEVICE = -5
 
 T5H_NUMERICS_DEFAULT = 0
 T5H_NUMERICS_HYBRID = 1
+T5H_NUMERICS_HYBRID_BF16 = 2
 
 
 class T5HConfig(C.Structure):

@@ -171,6 +171,8 @@ __device__ __forceinline__ float gelu_pade(float g) {
 // Host-side launchers (defined in the .hip files) --------------------------------
 namespace t5k {
 hipError_t launch_q4k_dequant(const void* blocks, size_t nblk, float* out, hipStream_t s);
+// Q4_K -> f32 (exact) -> bf16 truncation -> f16, [nblk * 256] in block order.
+hipError_t launch_q4k_dequant_bf16_f16(const void* blocks, size_t nblk, _Float16* out, hipStream_t s);
 // Tile plan of one batched GEMM launch: full tiles of 64*mw token rows x bn weight rows
 // cover rows [0, m_main); thin tiles of 16*tail_mb rows per math wave cover [m_main, M)
 // (tail_mb = 0: full tiles everywhere).

@@ -40,8 +40,16 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kMaxDevices] = {};
+// Per device: the event recorded after the last no-alloc call's launches (on that call's
+// stream), which the next no-alloc call's stream waits for before it touches the array, so
+// calls from different handles and threads run one after another on the GPU.  g_noalloc_mu[dev]
+// makes wait + enqueue + record one step for concurrent host threads.  Created with the
+// scratch mapping (at t5h_create), so the entry point itself creates nothing.
+hipEvent_t g_noalloc_ev[kMaxDevices] = {};
+std::mutex g_noalloc_mu[kMaxDevices];
 
-// Maps the scratch array on device `dev` (which must be current) once per process.
+// Maps the scratch array on device `dev` (which must be current) once per process, and creates
+// that device's ordering event.
 int scratch_init(int dev, void** out) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   *out = nullptr;
@@ -52,6 +60,12 @@ int scratch_init(int dev, void** out) {
     if (e != hipSuccess || !p)
       return fail(T5H_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
     g_scratch_dev[dev] = p;
+  }
+  if (!g_noalloc_ev[dev]) {
+    hipEvent_t ev = nullptr;
+    const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return fail(T5H_ERR_HIP, std::string("hipEventCreate(no-alloc order): ") + hipGetErrorString(e));
+    g_noalloc_ev[dev] = ev;
   }
   *out = g_scratch_dev[dev];
   return T5H_OK;
@@ -77,6 +91,11 @@ struct Linear {
   int fmt = WF_Q4K;
   size_t off = 0;         // byte offset in the weight arena
   const void* w = nullptr;  // device pointer (set after upload)
+  // F32/F16 dense weights also keep f16(bf16_trunc(w)) [N][K] for T5H_NUMERICS_HYBRID_BF16
+  // (the source values are only borrowed during t5h_create): arena offset, device pointer.
+  bool has_bf = false;
+  size_t bf_off = 0;
+  const void* bf = nullptr;
   size_t bytes() const { return fmt == WF_Q4K ? (size_t)N * K / QK_K * Q4K_BYTES : (size_t)N * K * 2; }
 };
 
@@ -206,6 +225,11 @@ struct t5h_model {
   double attn_flops = 0;   // QK^T + PV flops of one attention launch on the current batch, true tokens
   const float* final_ln = nullptr;
   std::vector<Layer> layers;
+  // The layers as T5H_NUMERICS_HYBRID_BF16 runs them: q/k/v/o/wo replaced by their f16 copies of
+  // the bf16-truncated weights (from the arena, or expanded from Q4_K into bfw), built on the
+  // first switch to that mode.
+  std::vector<Layer> layers_bf;
+  void* bfw = nullptr;
   Linear proj;
 
   // ---- workspace ----
@@ -276,6 +300,7 @@ struct t5h_model {
     for (auto e : event_pool) (void)hipEventDestroy(e);
     if (ws) (void)hipFree(ws);
     if (ew) (void)hipFree(ew);
+    if (bfw) (void)hipFree(bfw);
     if (arena) (void)hipFree(arena);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -359,6 +384,30 @@ int add_linear(HostArena& ha, const t5h::GgufFile& g, const std::string& name, i
   return T5H_OK;
 }
 
+// For an F32/F16 dense linear L (its source tensors `parts`, concatenated along N): a second
+// f16 copy of the weights truncated to bf16 first (bits & 0xffff0000, fbgemm-rs/src/bf16.rs:21-25),
+// which T5H_NUMERICS_HYBRID_BF16 uses in place of the round-to-nearest f16 copy.
+void add_bf16_copy(HostArena& ha, const std::vector<const t5h::GgufTensor*>& parts, Linear& L) {
+  if (L.fmt == WF_Q4K) return;
+  L.bf_off = ha.add(nullptr, (size_t)L.N * L.K * 2);
+  L.has_bf = true;
+  _Float16* dst = reinterpret_cast<_Float16*>(ha.bytes.data() + L.bf_off);
+  for (const t5h::GgufTensor* t : parts) {
+    const size_t ne = t->rows() * t->cols();
+    for (size_t i = 0; i < ne; i++) {
+      const float v = t->type == t5h::GGML_F32 ? reinterpret_cast<const float*>(t->data)[i]
+                                               : (float)reinterpret_cast<const _Float16*>(t->data)[i];
+      uint32_t u;
+      memcpy(&u, &v, 4);
+      u &= 0xffff0000u;
+      float tv;
+      memcpy(&tv, &u, 4);
+      dst[i] = (_Float16)tv;
+    }
+    dst += ne;
+  }
+}
+
 int add_f32_vector(HostArena& ha, const t5h::GgufFile& g, const std::string& name, size_t n,
                    size_t& off) {
   const t5h::GgufTensor* t = g.find(name);
@@ -432,6 +481,7 @@ int ensure_workspace(t5h_model* m, int T, int B, int nwork) {
     HIP_OK(hipFree(m->ws));
     m->last_B = -1;  // the device work list is gone
     m->ws = nullptr;
+    for (auto& r : m->replay) r = ReplayRec{};  // they point into the freed workspace
   }
   if (hipMalloc(&m->ws, off) != hipSuccess) {
     m->cap_tokens = m->cap_seqs = m->cap_work = 0;
@@ -534,6 +584,15 @@ bool fold_attn_norm(const t5h_model* m, int T) {
   (void)T;
   const int D = m->cfg.d_model;
   return !m->fold_norm_off && D % 64 == 0 && D <= NORM_REC_MAX_D;
+}
+
+// Both hybrid modes: Q8_K x Q4_K FFN gate|up and projection (T5H_NUMERICS_HYBRID_BF16 also runs
+// the dense linears on bf16-truncated weights, through layer_w).
+bool hybrid_numerics(const t5h_model* m) { return m->numerics != T5H_NUMERICS_DEFAULT; }
+
+// The weights block l runs with under the current numerics.
+const Layer& layer_w(const t5h_model* m, int l) {
+  return m->numerics == T5H_NUMERICS_HYBRID_BF16 ? m->layers_bf[l] : m->layers[l];
 }
 
 // Every norm folded.  With hybrid numerics the FFN's and the projection's Q8_K quantizer
@@ -829,9 +888,9 @@ int prenorm_rec(t5h_model* m, const float* w, int T, float* rec) {
 int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
               const float* next_gamma = nullptr) {
   const t5h_config& c = m->cfg;
-  const Layer& Ly = m->layers[l];
+  const Layer& Ly = layer_w(m, l);
   const int D = c.d_model, inner = m->inner;
-  const bool hybrid = m->numerics == T5H_NUMERICS_HYBRID;
+  const bool hybrid = hybrid_numerics(m);
   const bool fold = fold_norm(m, T), fold0 = fold_attn_norm(m, T);
   int rc;
   const float* nw0 = nullptr;
@@ -974,8 +1033,12 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
     if (s >= B || cu[s] <= cu[cut[parts - 1]] || cu[s] >= T) break;
     cut[parts++] = s;
   }
-  if (parts == 1) return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
   cut[parts] = B;
+  // A part small enough for the GEMV kernels would round differently from the batched GEMM the
+  // whole batch takes: keep one lane then, so results stay those of one lane.
+  for (int i = 0; i < parts && parts > 1; i++)
+    if (use_gemv(m, cu[cut[i + 1]] - cu[cut[i]])) parts = 1;
+  if (parts == 1) return enqueue_lane(m, d_ids, cu, B, T, d_out, d_norm, normalize);
   const int P = m->cfg.proj_dim;
   if (!m->ev_fork) HIP_OK(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
   for (int i = 0; i + 1 < parts; i++) {
@@ -1006,6 +1069,22 @@ int enqueue_forward(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int 
   return T5H_OK;
 }
 
+// The replay records of a profiled forward must not keep the caller's buffers (ids, outputs,
+// norms of t5h_encode_device or the embedder's buffers): the caller may free or reuse them before
+// t5h_replay_kernel runs.  Records that name them are pointed at the workspace's own buffers of
+// the same shape instead (ids copied there, so a replayed gather reads the same rows).
+int replay_own_buffers(t5h_model* m, const uint32_t* d_ids, int T, float* d_out, float* d_norm) {
+  if (d_ids != m->w.ids)
+    HIP_OK(hipMemcpyAsync(m->w.ids, d_ids, (size_t)T * 4, hipMemcpyDeviceToDevice, m->stream));
+  for (auto& r : m->replay) {
+    if (r.ids == d_ids) r.ids = m->w.ids;
+    if (d_out && r.ga.out == (void*)d_out) r.ga.out = m->w.out;
+    if (d_out && r.y == d_out) r.y = m->w.out;
+    if (d_norm && r.norm == d_norm) r.norm = m->w.norm;
+  }
+  return T5H_OK;
+}
+
 // The launches of one forward on the workspace m->w, whose attention work list (nwork items)
 // is in place.
 int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* d_out, float* d_norm,
@@ -1015,7 +1094,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
   // With folded norms the embedding gather also emits the first norm's operand and records
   // (hybrid numerics: when there is a block, whose QKV folds it; the projection's quantizer
   // normalises its own input).
-  const bool hybrid = m->numerics == T5H_NUMERICS_HYBRID;
+  const bool hybrid = hybrid_numerics(m);
   const bool fold = fold_norm(m, T) || (fold_attn_norm(m, T) && c.num_layers > 0);
   {
     // algorithmic bytes: the table rows read (f32, or 144 B per 256 values of a Q4_K table), x
@@ -1050,7 +1129,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
   }
   const float* nwf = nullptr;
   NormLink pn;
-  if (m->numerics == T5H_NUMERICS_HYBRID) {
+  if (hybrid) {
     if ((rc = hybrid_linear(m, K_GEMM_PROJ, m->final_ln, m->proj, nullptr, T, d_out, c.proj_dim))) return rc;
   } else {
     if (fold) {
@@ -1076,6 +1155,7 @@ int enqueue_stack(t5h_model* m, const uint32_t* d_ids, int T, int nwork, float* 
       r.normalize = normalize;
     }
   }
+  if (m->prof) return replay_own_buffers(m, d_ids, T, d_out, d_norm);
   return T5H_OK;
 }
 
@@ -1139,6 +1219,30 @@ int encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu
   m->w = saved;
   m->prof = prof;
   return rc;
+}
+
+// encode_device_noalloc ordered after every earlier no-alloc call on the same GPU (any handle,
+// any thread): the array's users form one chain through the device's event.  A stream under
+// graph capture is not chained (its launches run when the graph is replayed, not now): the
+// caller orders replays against other no-alloc work on that GPU.
+int encode_device_noalloc_ordered(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int B, float* d_out,
+                                  float* d_norm) {
+  int rc;
+  if ((rc = check_model(m))) return rc;
+  const int dev = m->device;
+  if (dev < 0 || dev >= kMaxDevices || !g_noalloc_ev[dev])
+    return fail(T5H_ERR_HIP, "no-alloc ordering event is not created on this device");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_OK(hipStreamIsCapturing(m->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone) return encode_device_noalloc(m, d_ids, cu, B, d_out, d_norm);
+  std::lock_guard<std::mutex> lk(g_noalloc_mu[dev]);
+  HIP_OK(hipStreamWaitEvent(m->stream, g_noalloc_ev[dev], 0));
+  rc = encode_device_noalloc(m, d_ids, cu, B, d_out, d_norm);
+  // recorded after a failed call too: whatever it enqueued stays ahead of the next user
+  const hipError_t e = hipEventRecord(g_noalloc_ev[dev], m->stream);
+  if (rc) return rc;
+  HIP_OK(e);
+  return T5H_OK;
 }
 
 int finish_sync(t5h_model* m) {
@@ -1418,8 +1522,14 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
       memcpy(tmp.data() + one, ha.bytes.data() + Ly.k.off, one);
       memcpy(tmp.data() + 2 * one, ha.bytes.data() + Ly.v.off, one);
       Ly.qkv.off = ha.add(tmp.data(), tmp.size());
+      add_bf16_copy(ha, {tq, tk, tv}, Ly.qkv);
+    } else {
+      add_bf16_copy(ha, {tq}, Ly.q);
+      add_bf16_copy(ha, {tk}, Ly.k);
+      add_bf16_copy(ha, {tv}, Ly.v);
     }
     if ((rc = add_linear(ha, g, p + "0.SelfAttention.o.weight", D, inner, Ly.o))) return rc;
+    add_bf16_copy(ha, {g.find(p + "0.SelfAttention.o.weight")}, Ly.o);
     if (cfg->feed_forward_gated) {
       if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi_0.weight", F, D, Ly.wi0))) return rc;
       if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi_1.weight", F, D, Ly.wi1))) return rc;
@@ -1428,6 +1538,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
       if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wi.weight", F, D, Ly.wi0))) return rc;
     }
     if ((rc = add_linear(ha, g, p + "1.DenseReluDense.wo.weight", D, F, Ly.wo))) return rc;
+    add_bf16_copy(ha, {g.find(p + "1.DenseReluDense.wo.weight")}, Ly.wo);
   }
   size_t fln_off;
   if ((rc = add_f32_vector(ha, g, "encoder.final_layer_norm.weight", D, fln_off))) return rc;
@@ -1439,7 +1550,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     return fail(T5H_ERR_NOMEM, "weight allocation of " + std::to_string(m->arena_bytes) + " bytes failed");
   HIP_OK(hipMemcpy(m->arena, ha.bytes.data(), ha.bytes.size(), hipMemcpyHostToDevice));
   uint8_t* base = (uint8_t*)m->arena;
-  auto bind = [&](Linear& L) { L.w = base + L.off; };
+  auto bind = [&](Linear& L) {
+    L.w = base + L.off;
+    if (L.has_bf) L.bf = base + L.bf_off;
+  };
   m->emb = base + emb_off;
   m->rel_lut = (const float*)(base + lut_off);
   m->lutw = lutw;
@@ -1554,7 +1668,7 @@ int t5h_encode_device(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, in
 
 int t5h_encode_device_noalloc(t5h_model* m, const uint32_t* d_ids, const int32_t* cu, int32_t B, float* d_out,
                               float* d_norm) {
-  return encode_device_noalloc(m, d_ids, cu, B, d_out, d_norm);
+  return encode_device_noalloc_ordered(m, d_ids, cu, B, d_out, d_norm);
 }
 
 int t5h_synchronize(t5h_model* m) {
@@ -1662,11 +1776,11 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   if (!m->cfg.feed_forward_gated) return fail(T5H_ERR_INVALID, "model FFN is not gated");
   if ((rc = ensure_workspace(m, T, 1, attn_work_cap(m, T, 1)))) return rc;
   const t5h_config& c = m->cfg;
-  const Layer& Ly = m->layers[layer];
+  const Layer& Ly = layer_w(m, layer);
   const size_t bytes = (size_t)T * c.d_model * 4;
   HIP_OK(hipMemcpyAsync(m->w.x, x, bytes, hipMemcpyHostToDevice, m->stream));
   m->batched_only = mode == 1;
-  if (m->numerics == T5H_NUMERICS_HYBRID) {
+  if (hybrid_numerics(m)) {
     rc = hybrid_linear(m, K_GEMM_GATE_UP, nullptr, Ly.wi0, &Ly.wi1, T, nullptr, 0);
   } else {
     HIP_OK(t5k::launch_f32_to_f16(m->w.x, m->w.xn, (size_t)T * c.d_model, c.d_model, m->stream));
@@ -1679,6 +1793,51 @@ int t5h_ffn_block(t5h_model* m, int32_t layer, const float* x, int32_t T, float*
   return finish_sync(m);
 }
 
+namespace {
+// The dense linears of T5H_NUMERICS_HYBRID_BF16 (q/k/v or the fused qkv, o, wo): F32/F16 ones
+// point at their arena copy of the truncated weights; Q4_K ones are expanded once into bfw
+// (dequantized exactly, truncated to bf16, stored as f16 [N][K]).  Synchronous.
+int build_bf16_layers(t5h_model* m) {
+  if (!m->layers_bf.empty()) return T5H_OK;
+  std::vector<Layer> lb = m->layers;
+  std::vector<Linear*> dense;
+  for (Layer& Ly : lb) {
+    if (Ly.fused_qkv) {
+      dense.push_back(&Ly.qkv);
+    } else {
+      dense.push_back(&Ly.q);
+      dense.push_back(&Ly.k);
+      dense.push_back(&Ly.v);
+    }
+    dense.push_back(&Ly.o);
+    dense.push_back(&Ly.wo);
+  }
+  size_t need = 0;
+  for (const Linear* L : dense)
+    if (L->fmt == WF_Q4K) need += align256((size_t)L->N * L->K * 2);
+  if (need && hipMalloc(&m->bfw, need) != hipSuccess) {
+    m->bfw = nullptr;
+    return fail(T5H_ERR_NOMEM, "bf16 weight allocation of " + std::to_string(need) + " bytes failed");
+  }
+  size_t off = 0;
+  for (Linear* L : dense) {
+    if (L->fmt == WF_Q4K) {
+      _Float16* dst = (_Float16*)((uint8_t*)m->bfw + off);
+      HIP_OK(t5k::launch_q4k_dequant_bf16_f16(L->w, (size_t)L->N * L->K / QK_K, dst, m->stream));
+      off += align256((size_t)L->N * L->K * 2);
+      L->w = dst;
+    } else {
+      if (!L->has_bf) return fail(T5H_ERR_INVALID, "internal: dense linear without its bf16 copy");
+      L->w = L->bf;
+    }
+    L->fmt = WF_F16;
+  }
+  HIP_OK(hipStreamSynchronize(m->stream));
+  m->layers_bf = std::move(lb);
+  return T5H_OK;
+}
+}  // namespace
+
 int t5h_set_numerics(t5h_model* m, int32_t mode) {
   int rc;
   if ((rc = check_model(m))) return rc;
@@ -1687,7 +1846,8 @@ int t5h_set_numerics(t5h_model* m, int32_t mode) {
     m->numerics = mode;
     return T5H_OK;
   }
-  if (mode != T5H_NUMERICS_HYBRID) return fail(T5H_ERR_INVALID, "unknown numerics mode");
+  if (mode != T5H_NUMERICS_HYBRID && mode != T5H_NUMERICS_HYBRID_BF16)
+    return fail(T5H_ERR_INVALID, "unknown numerics mode");
   const t5h_config& c = m->cfg;
   if (!c.feed_forward_gated) return fail(T5H_ERR_INVALID, "hybrid numerics: the FFN must be gated-gelu");
   for (const Layer& Ly : m->layers)
@@ -1701,6 +1861,7 @@ int t5h_set_numerics(t5h_model* m, int32_t mode) {
   if ((size_t)(c.d_model / QK_K) * 68 + 2 > (size_t)m->inner * 2)
     return fail(T5H_ERR_INVALID, "hybrid numerics: the Q8_K scales do not fit the attention output buffer");
   HIP_OK(hipStreamSynchronize(m->stream));
+  if (mode == T5H_NUMERICS_HYBRID_BF16 && (rc = build_bf16_layers(m))) return rc;
   m->numerics = mode;
   return T5H_OK;
 }

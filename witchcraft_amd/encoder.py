@@ -149,8 +149,10 @@ class T5EncoderModel:
         return [(out[koff[d]:koff[d + 1]], kept[koff[d]:koff[d + 1]]) for d in range(len(docs))]
 
     def set_numerics(self, mode: int) -> None:
-        """T5H_NUMERICS_DEFAULT (t5-quantized) or T5H_NUMERICS_HYBRID (hybrid-dequant: Q8_K x Q4_K
-        integer dot products for wi_0 / wi_1 and the projection, Pade gelu)."""
+        """T5H_NUMERICS_DEFAULT (t5-quantized), T5H_NUMERICS_HYBRID (hybrid-dequant: Q8_K x Q4_K
+        integer dot products for wi_0 / wi_1 and the projection, Pade gelu) or
+        T5H_NUMERICS_HYBRID_BF16 (hybrid-dequant + fbgemm: the same, with q/k/v/o/wo truncated to
+        bf16)."""
         check(lib.t5h_set_numerics(self._h, int(mode)))
 
     # ---- test hooks ----
