@@ -86,31 +86,38 @@ def _time_per_sequence(fn, ids, cu, budget_s: float):
     return tok, secs, used
 
 
-def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_s: float) -> dict:
+def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_s: float,
+                 variants_run=("f32_torch", "f32_c", "hybrid_bf16_c")) -> dict:
     """The reference's CPU encoder numerics timed on this host, per sequence as the reference
-    runs them.  Three restatements (test infrastructure under oracle/):
+    runs them, split evenly over the restatements named in `variants_run` (test infrastructure
+    under oracle/):
       f32_torch     -- the default t5-quantized path (Q4_K dequantized to f32 at load, f32 GEMMs,
                        src/quantized_t5.rs:39-49) on torch's multithreaded CPU GEMMs: the
-                       strong-BLAS figure, reported as `value`;
+                       strong-BLAS figure;
       f32_c         -- the same path in the C oracle's loops (OpenMP over output rows);
-      hybrid_bf16_c -- the x86 default build (hybrid-dequant + fbgemm, Makefile:26-30): Q8_K x
-                       Q4_K integer dots for wi_0/wi_1/linear with the Pade gelu, bf16-truncated
-                       q/k/v/o/wo (src/fused_matmul.rs:138-177, fbgemm-rs/src/bf16.rs:21-25),
-                       in the C oracle's scalar loops (no fbgemm assembly kernels).
+      hybrid_c      -- the hybrid-dequant feature: Q8_K x Q4_K integer dots for wi_0/wi_1/linear
+                       with the Pade gelu, f32 q/k/v/o/wo (src/fused_matmul.rs:27-59,138-177);
+      hybrid_bf16_c -- the x86 default build (hybrid-dequant + fbgemm, Makefile:26-30): the same
+                       with bf16-truncated q/k/v/o/wo (fbgemm-rs/src/bf16.rs:21-25), in the C
+                       oracle's scalar loops (no fbgemm assembly kernels).
     The value is the fastest variant, so the GPU/CPU ratio is the least flattering one."""
     from oracle import oracle as orc
-    from oracle.torch_port import TorchCpuEncoder
 
     info = cpu_info()
     threads = info["threads"]
     used_omp = orc.set_threads(threads)
     variants = {}
-    share = budget_s / 3
-    port = TorchCpuEncoder(img, cfg, threads=threads)
-    tok, secs, n = _time_per_sequence(port.forward, ids, cu, share)
-    variants["f32_torch"] = {"tokens_per_s": tok / secs, "sequences": n, "tokens": tok, "threads": threads}
-    del port
-    for name, var in (("f32_c", orc.VARIANT_DEFAULT), ("hybrid_bf16_c", orc.VARIANT_HYBRID_BF16)):
+    share = budget_s / len(variants_run)
+    for name in variants_run:
+        if name == "f32_torch":
+            from oracle.torch_port import TorchCpuEncoder
+            port = TorchCpuEncoder(img, cfg, threads=threads)
+            tok, secs, n = _time_per_sequence(port.forward, ids, cu, share)
+            del port
+            variants[name] = {"tokens_per_s": tok / secs, "sequences": n, "tokens": tok, "threads": threads}
+            continue
+        var = {"f32_c": orc.VARIANT_DEFAULT, "hybrid_c": orc.VARIANT_HYBRID,
+               "hybrid_bf16_c": orc.VARIANT_HYBRID_BF16}[name]
         m = orc.OracleModel(img, cfg, variant=var)
         tok, secs, n = _time_per_sequence(lambda s: m.forward(s, acc64=False), ids, cu, share)
         m.close()
@@ -126,12 +133,15 @@ def cpu_baseline(img: bytes, cfg: dict, ids: np.ndarray, cu: np.ndarray, budget_
 
 
 def kernel_table(model, step, n: int, reps: int = 20, unit: str = "step") -> dict:
-    """Per kernel class: launches per step, and the average launch duration from `reps`
-    back-to-back relaunches of the class's last launch in a profiled forward, between two HIP
-    events on the model's stream (t5h_replay_kernel).  event_avg_us is the same class timed by
-    events around every launch inside the forwards, which adds each launch's dispatch and
-    completion latency; the relaunch figure is the one comparable with rocprofv3's
-    per-dispatch durations.  Algorithmic FLOP and bytes per launch come from the library."""
+    """Per kernel class: launches per step, and the average in-forward launch duration over `n`
+    profiled forwards.  The library times each launch by HIP events bound to the kernel dispatch
+    itself (hipExtLaunchKernelGGL start/stop events on the model's stream), so avg_us is the
+    kernel's execution time inside the forward, the figure rocprofv3's kernel trace reports for
+    the same dispatches.  relaunch_avg_us: `reps` back-to-back relaunches of the class's last
+    launch (t5h_replay_kernel), which run a few percent faster than inside the forward (the
+    kernel's operands stay warm in L2 and the MALL).  Profiled forwards run on one lane, so a
+    batch that normally splits across two streams is timed kernel by kernel on one.  Algorithmic
+    FLOP and bytes per launch come from the library."""
     model.set_profiling(True)
     for _ in range(n):
         step()
@@ -141,10 +151,10 @@ def kernel_table(model, step, n: int, reps: int = 20, unit: str = "step") -> dic
     for name, s in stats.items():
         if not s["launches"]:
             continue
-        us = model.replay_kernel(s["kind"], reps)
+        us = s["total_ms"] / s["launches"] * 1e3
         per = s["launches"] / n
         k = {f"launches_per_{unit}": per, "avg_us": us, "ms_per_step": us * per * 1e-3,
-             "event_avg_us": s["total_ms"] / s["launches"] * 1e3}
+             "relaunch_avg_us": model.replay_kernel(s["kind"], reps)}
         if s["flops"]:
             k["flops_per_launch"] = s["flops"] / s["launches"]
             k["tflops"] = k["flops_per_launch"] / (us * 1e-6) / 1e12
@@ -159,6 +169,56 @@ def kernel_table(model, step, n: int, reps: int = 20, unit: str = "step") -> dic
 
 
 QUERY_BYTES = 47_947_392  # cfg3 per query: Q4_K weights + embedding rows + bias table + output + ids
+
+
+def query_kernel_table(models, query, n: int) -> dict:
+    """kernel_table for the query regime: `n` profiled queries cycling over every replica (so the
+    GEMVs stream their weights as the timed queries do), per-class stats summed over the replicas;
+    relaunch_avg_us from replica 0 (its weights warm in the MALL after the first relaunch)."""
+    for m in models:
+        m.set_profiling(True)
+    for i in range(n):
+        query(i)
+    for m in models:
+        m.synchronize()
+    acc = {}
+    for m in models:
+        for name, st in m.kernel_stats().items():
+            a = acc.setdefault(name, {"kind": st["kind"], "launches": 0, "total_ms": 0.0, "flops": 0.0, "bytes": 0.0})
+            for f in ("launches", "total_ms", "flops", "bytes"):
+                a[f] += st[f]
+    out = {}
+    for name, st in acc.items():
+        if not st["launches"]:
+            continue
+        us = st["total_ms"] / st["launches"] * 1e3
+        per = st["launches"] / n
+        k = {"launches_per_query": per, "avg_us": us, "ms_per_step": us * per * 1e-3,
+             "relaunch_avg_us": models[0].replay_kernel(st["kind"], 20)}
+        if st["flops"]:
+            k["flops_per_launch"] = st["flops"] / st["launches"]
+            k["tflops"] = k["flops_per_launch"] / (us * 1e-6) / 1e12
+            k["mfma_frac"] = k["tflops"] / PEAK_F16_TFLOPS
+        if st["bytes"]:
+            k["bytes_per_launch"] = st["bytes"] / st["launches"]
+            k["gbs"] = k["bytes_per_launch"] / (us * 1e-6) / 1e9
+            k["hbm_frac"] = k["gbs"] / PEAK_HBM_GBS
+        out[name] = k
+    for m in models:
+        m.set_profiling(False)
+    return out
+
+
+def profiled_traffic(tag: str, cls: str, applies: bool):
+    """HBM bytes per dispatch of kernel class `cls` from profiles/<tag>_traffic.json (rocprofv3
+    FETCH_SIZE and WRITE_SIZE passes of this workload through bench.py --counter-pass, each scaled
+    by the same counter's reading for a plain copy of known size; bench.py --summarize writes the
+    file), or None when there is no such pass for this exact workload."""
+    f = ROOT / "profiles" / f"{tag}_traffic.json"
+    if not applies or not f.exists():
+        return None
+    t = json.loads(f.read_text())["bytes_per_dispatch"].get(cls)
+    return t["fetch"] + t["write"] if t else None
 
 
 def run_query(args, img: bytes | None = None, cpu: bool = True) -> dict:
@@ -204,10 +264,9 @@ def run_query(args, img: bytes | None = None, cpu: bool = True) -> dict:
     p50, p95 = float(np.percentile(lat, 50) * 1e6), float(np.percentile(lat, 95) * 1e6)
     log(f"[bench] cfg3: {args.queries} queries over {len(models)} replicas: p50 {p50:.1f} us, p95 {p95:.1f} us")
 
-    # per-kernel durations (one replica) -> dominant GEMV class vs the HBM roofline.  The
-    # relaunches of one kernel read its weights from the MALL after the first, so these are
-    # warm-cache figures; the latency above is the cold (rotated) one.
-    kernels = kernel_table(models[0], lambda: query(0), 20, unit="query")
+    # per-kernel in-forward durations over rotated queries (weights streamed as in the timed
+    # queries) -> dominant GEMV class vs the HBM roofline
+    kernels = query_kernel_table(models, query, 10 * len(models))
     for mm in models:
         mm.close()
     gemv = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
@@ -223,7 +282,8 @@ def run_query(args, img: bytes | None = None, cpu: bool = True) -> dict:
            "whole_query_hbm_frac": QUERY_BYTES / (p50 * 1e-6) / 1e9 / PEAK_HBM_GBS,
            "roofline": {"kernel": f"{dom_name} (Q4_K GEMV, M = 32)", "bound": "hbm", "achieved": achieved,
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
-                        "traffic": None, "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
+                        "traffic": profiled_traffic("query_cfg3", dom_name, args.seed == 0 and len(models) == 8),
+                        "bytes_per_launch": bytes_per_launch, "avg_launch_us": avg_s * 1e6},
            "kernels": kernels, "cpu_baseline": None}
     if cpu and not args.no_cpu_baseline:
         from oracle.torch_port import TorchCpuEncoder
@@ -549,6 +609,205 @@ def codec_bench(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+NUMERICS = {"default": 0, "hybrid": 1, "hybrid_bf16": 2}
+
+
+def run_batched(args, workload: str, numerics: str, steps: int, warmup: int, cpu_variants=None,
+                cpu_budget: float = 0.0, img: bytes | None = None) -> dict:
+    """One batched workload (cfg2 / cfg4 / cfg5): `warmup` untimed forwards, then `steps` forwards
+    timed from the host between device synchronisations (whole-job tokens/s, ids resident in
+    HBM), then the per-class in-forward kernel table, the dominant GEMM class against its
+    matrix-core roofline, and the CPU baseline on a bounded sample (cpu_variants, or none)."""
+    import torch
+
+    from witchcraft_amd import synth
+    from witchcraft_amd.encoder import T5EncoderModel
+
+    n_seqs, lo, hi, pad, desc = WORKLOADS[workload]
+    cfg = dict(synth.XTR_BASE)
+    if img is None:
+        t0 = time.perf_counter()
+        img = synth.make_model(cfg, seed=args.seed, layout="hybrid" if workload == "cfg5" else "q4k")
+        log(f"[bench] {workload}: model built in {time.perf_counter() - t0:.1f}s ({len(img) / 1e6:.1f} MB GGUF)")
+    model = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
+    model.set_numerics(NUMERICS[numerics])
+    ids, cu = synth.ragged_batch(n_seqs, lo, hi, cfg["vocab_size"], seed=1000 + args.seed)
+    T = int(cu[-1])
+    dev = torch.device("cuda:0")
+    d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+    d_out = torch.empty((T, cfg["proj_dim"]), dtype=torch.float32, device=dev)
+    d_norm = torch.empty(T, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def step():
+        model.encode_device(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+
+    for _ in range(warmup):
+        step()
+    model.synchronize()
+
+    # ---- timed region: whole-job throughput ----
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        step()
+    model.synchronize()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    ms_per_step = elapsed / steps * 1e3
+    value = T * steps / elapsed
+    log(f"[bench] {workload} ({numerics}): {steps} steps, {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
+    res = {"workload": f"{workload}: {desc}", "value": value, "unit": "tokens/s", "ms_per_step": ms_per_step,
+           "steps": steps, "warmup": warmup, "tokens_per_step": T, "global_batch": n_seqs, "seq_len": pad,
+           "numerics": numerics}
+    if args.counter_pass:
+        model.close()
+        return res
+
+    # ---- per-kernel in-forward durations; dominant GEMM class vs the matrix-core roofline ----
+    kernels = kernel_table(model, step, min(steps, 10))
+    model.close()
+    gemms = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
+    dom_name = max(gemms, key=lambda k: gemms[k]["ms_per_step"])
+    dom = gemms[dom_name]
+    avg_s = dom["avg_us"] * 1e-6
+    flops_per_launch = dom["flops_per_launch"]
+    achieved = flops_per_launch / avg_s / 1e12
+    tag = f"encoder_{workload}" + ("" if numerics == "default" else f"_{numerics}")
+    applies = args.seed == 0
+    counters = None
+    tfile = ROOT / "profiles" / f"{tag}_traffic.json"
+    if applies and tfile.exists():
+        c = json.loads(tfile.read_text()).get("counters", {}).get(dom_name)
+        if c:
+            # MFMA work the counters saw the class's launches execute, over the in-forward duration
+            # measured here, and the share of SIMD cycles the matrix cores were busy
+            counters = {"mfma_flop_executed": c["mfma_flop_executed"],
+                        "tflops_executed": c["mfma_flop_executed"] / avg_s / 1e12,
+                        "frac_executed": c["mfma_flop_executed"] / avg_s / 1e12 / PEAK_F16_TFLOPS,
+                        "mfma_busy_frac": c["mfma_busy_frac"],
+                        "source": f"profiles/{tag}_traffic.json (rocprofv3 --pmc through bench.py)"}
+    roofline = {"kernel": f"{dom_name} (Q4_K dequant-GEMM, v_mfma_f32_16x16x32_f16)",
+                "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / PEAK_F16_TFLOPS, "traffic": profiled_traffic(tag, dom_name, applies),
+                "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6,
+                "relaunch_avg_us": dom["relaunch_avg_us"],
+                "share_of_step": dom["ms_per_step"] / sum(v["ms_per_step"] for v in kernels.values()),
+                "counters": counters}
+    if numerics != "default" and dom_name in ("gemm_ffn_gate_up", "gemm_proj"):
+        # the hybrid FFN's products run as int8 MFMAs (two weight planes per product, so the
+        # matrix cores execute twice the algorithmic ops counted here), after the Q8_K quantizer
+        roofline.update({"kernel": f"{dom_name} (Q8_K quantize + Q4_K x Q8_K on v_mfma_i32_16x16x64_i8)",
+                         "unit": "TOP/s", "peak": PEAK_INT8_TOPS, "frac": achieved / PEAK_INT8_TOPS})
+    res.update({"roofline": roofline, "kernels": kernels, "cpu_baseline": None})
+    if cpu_variants and not args.no_cpu_baseline:
+        log(f"[bench] {workload}: CPU baseline ({', '.join(cpu_variants)}, bounded sample) ...")
+        res["cpu_baseline"] = cpu_baseline(img, cfg, ids, cu, cpu_budget, cpu_variants)
+    res["_img"] = img
+    return res
+
+
+def summarize(args) -> None:
+    """Reads rocprofv3 CSV output (kernel trace and/or counter collection, each pass in its own
+    directory) and prints, per encoder kernel class, the average dispatch duration and the
+    counters per dispatch; with --copy-fetch / --copy-write (passes of --copy-calibration) the
+    FETCH_SIZE / WRITE_SIZE readings are scaled to bytes by the copy's known size.  --out writes
+    the bytes per dispatch as the JSON file the bench line reads (profiles/<tag>_traffic.json)."""
+    import csv
+    import glob
+    import re
+
+    def rows(d, suffix):
+        fs = glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)
+        if not fs:
+            raise SystemExit(f"summarize: no *{suffix} under {d}")
+        out = []
+        for f in fs:
+            out += list(csv.DictReader(open(f)))
+        return out
+
+    def base_class(name):
+        m = re.search(r"(gemm|gemv)_kernel(?:<|ILi)(-?\d+)", name)
+        if m:
+            return {"4": "gemm_qkv", "2": "gemm_ffn_gate_up", "5": "gemm_ffn_gate_up", "3": "gemm_proj",
+                    "1": "resid"}.get(m.group(2))
+        for key, cls in (("embed_kernel", "embed_gather"), ("rownorm_kernel", "rownorm"),
+                         ("rmsnorm_kernel", "rmsnorm"), ("attn_relbias_kernel", "attention"),
+                         ("q8k_quantize_kernel", "q8k_quantize"), ("copyBuffer", "copy")):
+            if key in name:
+                return key if cls is None else cls
+        return None
+
+    def classify(rs, name_key, id_key):
+        """Dispatch id -> class; the residual GEMM/GEMV is O after attention and FFN wo after the
+        gated FFN (the forward's launch order; relaunches of one class follow each other)."""
+        cls, prev = {}, None
+        for r in sorted(rs, key=lambda r: int(r[id_key])):
+            c = base_class(r[name_key])
+            if c == "resid":
+                c = "gemm_o" if prev in ("attention", "gemm_o") else "gemm_ffn_wo"
+            if c:
+                cls[int(r[id_key])] = c
+                if c != "copy":
+                    prev = c
+        return cls
+
+    summary = {"workload": args.summarize_workload, "classes": {}}
+    if args.trace:
+        tr = rows(args.trace, "kernel_trace.csv")
+        cls = classify(tr, "Kernel_Name", "Dispatch_Id")
+        acc = {}
+        for r in tr:
+            c = cls.get(int(r["Dispatch_Id"]))
+            if c:
+                a = acc.setdefault(c, [])
+                a.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+        for c, v in acc.items():
+            summary["classes"].setdefault(c, {}).update({"dispatches": len(v), "avg_us": sum(v) / len(v),
+                                                         "total_ms": sum(v) * 1e-3})
+
+    def per_dispatch(d):
+        rs = rows(d, "counter_collection.csv")
+        cls = classify({int(r["Dispatch_Id"]): r for r in rs}.values(), "Kernel_Name", "Dispatch_Id")
+        acc = {}
+        for r in rs:
+            c = cls.get(int(r["Dispatch_Id"]))
+            if c:
+                acc.setdefault(c, {}).setdefault(r["Counter_Name"], {}).setdefault(int(r["Dispatch_Id"]), 0.0)
+                acc[c][r["Counter_Name"]][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+        return {c: {k: sum(v.values()) / len(v) for k, v in cc.items()} for c, cc in acc.items()}
+
+    scale = {}
+    for key, d in (("FETCH_SIZE", args.copy_fetch), ("WRITE_SIZE", args.copy_write)):
+        if d:
+            kib = per_dispatch(d)["copy"][key]
+            scale[key] = args.copy_bytes / (kib * 1024.0)
+    for d in args.counters or []:
+        for c, vals in per_dispatch(d).items():
+            summary["classes"].setdefault(c, {}).update(vals)
+    traffic = {}
+    for c, v in summary["classes"].items():
+        if "FETCH_SIZE" in v and "WRITE_SIZE" in v and scale:
+            traffic[c] = {"fetch": v["FETCH_SIZE"] * 1024 * scale.get("FETCH_SIZE", 1.0),
+                          "write": v["WRITE_SIZE"] * 1024 * scale.get("WRITE_SIZE", 1.0)}
+        if "SQ_INSTS_VALU_MFMA_F16" in v:
+            v["mfma_flop_executed"] = v["SQ_INSTS_VALU_MFMA_F16"] * 16 * 16 * 32 * 2
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in v and "GRBM_GUI_ACTIVE" in v:
+            v["mfma_busy_frac"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * v["GRBM_GUI_ACTIVE"] / 8)
+    summary["scale"] = scale
+    summary["bytes_per_dispatch"] = traffic
+    print(json.dumps(summary, indent=1))
+    if args.out:
+        counters = {c: {k: v[k] for k in ("mfma_flop_executed", "mfma_busy_frac") if k in v}
+                    for c, v in summary["classes"].items() if "mfma_flop_executed" in v and "mfma_busy_frac" in v}
+        Path(args.out).write_text(json.dumps({
+            "workload": args.summarize_workload,
+            "source": "rocprofv3 --pmc passes of bench.py --counter-pass, summarised by bench.py --summarize",
+            "fetch_scale": scale.get("FETCH_SIZE"), "write_scale": scale.get("WRITE_SIZE"),
+            "bytes_per_dispatch": traffic, "counters": counters,
+            "trace_avg_us": {c: v["avg_us"] for c, v in summary["classes"].items() if "avg_us" in v}}, indent=1) + "\n")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -561,9 +820,15 @@ def main() -> None:
     ap.add_argument("--queries", type=int, default=1000, help="cfg3: number of timed queries")
     ap.add_argument("--rotate", type=int, default=8, help="cfg3: model replicas cycled (MALL defeat)")
     ap.add_argument("--no-query", action="store_true", help="cfg2: leave out the cfg3 query object")
-    ap.add_argument("--numerics", default="default", choices=["default", "hybrid"],
+    ap.add_argument("--no-configs", action="store_true",
+                    help="cfg2: leave out the cfg4 / cfg5 objects of the default line")
+    ap.add_argument("--numerics", default="default", choices=sorted(NUMERICS),
                     help="batched workloads: t5h_set_numerics mode (hybrid: the hybrid-dequant "
-                         "feature's Q8_K x Q4_K FFN and projection)")
+                         "feature's Q8_K x Q4_K FFN and projection; hybrid_bf16: also bf16-truncated "
+                         "q/k/v/o/wo, the x86 hybrid-dequant + fbgemm build)")
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="only the warmup and timed forwards (cfg3: the rotated queries) of the workload, "
+                         "for rocprofv3 --pmc passes whose dispatches should all be that workload's")
     ap.add_argument("--score-n", type=int, default=1 << 20, help="score: residual rows")
     ap.add_argument("--kmeans-m", type=int, default=1 << 17, help="score: k-means rows")
     ap.add_argument("--kmeans-k", type=int, default=1 << 14, help="score: k-means centers")
@@ -572,7 +837,20 @@ def main() -> None:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 10 times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--summarize", action="store_true",
+                    help="summarise rocprofv3 CSV output (no GPU): --trace DIR, --counters DIR..., "
+                         "--copy-fetch DIR / --copy-write DIR (passes of --copy-calibration), --out FILE")
+    ap.add_argument("--trace", default=None)
+    ap.add_argument("--counters", nargs="*", default=None)
+    ap.add_argument("--copy-fetch", default=None)
+    ap.add_argument("--copy-write", default=None)
+    ap.add_argument("--copy-bytes", type=float, default=256 * (1 << 20))
+    ap.add_argument("--summarize-workload", default="")
+    ap.add_argument("--out", default=None)
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args)
+        return
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
@@ -589,7 +867,10 @@ def main() -> None:
         sys.exit(2)
 
     if args.workload == "cfg3":
-        query_bench(args)
+        if args.counter_pass:
+            run_query_counter_pass(args)
+        else:
+            query_bench(args)
         return
     if args.workload == "score":
         score_bench(args)
@@ -601,108 +882,71 @@ def main() -> None:
         embed_bench(args)
         return
 
+    w = args.workload
+    main_cpu = ("f32_torch", "f32_c", "hybrid_bf16_c") if args.numerics == "default" else \
+        (("hybrid_c",) if args.numerics == "hybrid" else ("hybrid_bf16_c",))
+    r = run_batched(args, w, args.numerics, args.steps, args.warmup, main_cpu, args.cpu_budget)
+    if args.counter_pass:
+        print(json.dumps({"counter_pass": w, "numerics": args.numerics, "value": r["value"],
+                          "tokens_per_step": r["tokens_per_step"]}), flush=True)
+        return
+    img = r.pop("_img")
+    line = {
+        "metric": METRIC, "value": r["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16" if args.numerics == "default" else "f16+int8", "data": "synthetic",
+        "config": {"workload": r["workload"], "global_batch": r["global_batch"], "seq_len": r["seq_len"],
+                   "tokens_per_step": r["tokens_per_step"],
+                   "weights": "random-init N(0,0.02^2), Q4_K by the quantize tool's scale/min search "
+                              "(t5h_quantize_q4k); f32 embeddings and norms",
+                   "numerics": args.numerics, "parallelism": "single GPU"},
+        "roofline": r["roofline"], "cpu_baseline": r["cpu_baseline"], "kernels": r["kernels"],
+    }
+    if w == "cfg2" and not args.no_configs:
+        # The compute-bound configurations beside the headline, each timed the same way (fewer
+        # steps), with its dominant GEMM's in-forward roofline and a small CPU sample.
+        extra = {}
+        budget = min(args.cpu_budget, 4.0)
+        r4 = run_batched(args, "cfg4", "default", 10, 3, ("f32_torch",), budget)
+        r4.pop("_img")
+        extra["cfg4"] = r4
+        img5 = None
+        for num, cv in (("default", ("f32_torch",)), ("hybrid", ("hybrid_c",)), ("hybrid_bf16", ("hybrid_bf16_c",))):
+            r5 = run_batched(args, "cfg5", num, 10, 3, cv, budget, img=img5)
+            img5 = r5.pop("_img")
+            extra["cfg5" if num == "default" else f"cfg5_{num}"] = r5
+        line["configs"] = extra
+    if w == "cfg2" and not args.no_query:
+        line["query"] = run_query(args, img if args.seed == 0 else None)
+    print(json.dumps(line), flush=True)
+
+
+def run_query_counter_pass(args) -> None:
+    """cfg3 for rocprofv3 --pmc passes: the rotated queries only (no profiled queries, relaunches
+    or CPU leg), so every dispatch of the run streams its weights as a timed query does."""
     import torch
 
     from witchcraft_amd import synth
     from witchcraft_amd.encoder import T5EncoderModel
 
-    n_seqs, lo, hi, pad, desc = WORKLOADS[args.workload]
     cfg = dict(synth.XTR_BASE)
-    t0 = time.perf_counter()
-    img = synth.make_model(cfg, seed=args.seed, layout="hybrid" if args.workload == "cfg5" else "q4k")
-    log(f"[bench] model built in {time.perf_counter() - t0:.1f}s ({len(img) / 1e6:.1f} MB GGUF)")
-    model = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
-    if args.numerics == "hybrid":
-        model.set_numerics(1)
-    ids, cu = synth.ragged_batch(n_seqs, lo, hi, cfg["vocab_size"], seed=1000 + args.seed)
-    T = int(cu[-1])
+    img = synth.make_model(cfg, seed=args.seed)
+    models = [T5EncoderModel.from_gguf(img, cfg, hip_device=0) for _ in range(args.rotate)]
+    L = 32
+    pool = np.random.default_rng(2000 + args.seed).integers(1, cfg["vocab_size"], size=(64, L)).astype(np.int32)
+    cu = np.array([0, L], np.int32)
     dev = torch.device("cuda:0")
-    d_ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
-    d_out = torch.empty((T, cfg["proj_dim"]), dtype=torch.float32, device=dev)
-    d_norm = torch.empty(T, dtype=torch.float32, device=dev)
+    d_ids = [torch.from_numpy(q).to(dev) for q in pool]
+    d_out = torch.empty((L, cfg["proj_dim"]), dtype=torch.float32, device=dev)
+    d_norm = torch.empty(L, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
-
-    def step():
-        model.encode_device(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
-
-    for _ in range(args.warmup):
-        step()
-    model.synchronize()
-    log(f"[bench] warmup done ({args.warmup} steps, T={T} tokens)")
-
-    # ---- timed region: whole-job throughput ----
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    model.synchronize()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t
-    ms_per_step = elapsed / args.steps * 1e3
-    value = T * args.steps / elapsed
-    log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
-
-    # ---- per-kernel durations with HIP events on the model stream ----
-    kernels = kernel_table(model, step, args.steps)
-    # dominant kernel = the GEMM class with the largest share of the step
-    gemms = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
-    dom_name = max(gemms, key=lambda k: gemms[k]["ms_per_step"])
-    dom = gemms[dom_name]
-    avg_s = dom["avg_us"] * 1e-6
-    flops_per_launch = dom["flops_per_launch"]
-    achieved = flops_per_launch / avg_s / 1e12
-    traffic = None
-    counters = None
-    tfile = ROOT / "profiles" / "encoder_cfg2_traffic.json"
-    if args.workload == "cfg2" and args.seed == 0 and tfile.exists():
-        tj = json.loads(tfile.read_text())
-        t = tj["bytes_per_dispatch"].get(dom_name)
-        traffic = t["fetch"] + t["write"] if t else None
-        c = tj.get("counters_gate_up")
-        if c and dom_name == "gemm_ffn_gate_up":
-            # MFMA work the counters saw this launch execute (instructions x 16x16x32 x 2),
-            # over the launch duration measured here
-            counters = {"mfma_flop_executed": c["mfma_flop_executed"],
-                        "tflops_executed": c["mfma_flop_executed"] / avg_s / 1e12,
-                        "frac_executed": c["mfma_flop_executed"] / avg_s / 1e12 / PEAK_F16_TFLOPS,
-                        "mfma_busy_frac": c["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * c["GRBM_GUI_ACTIVE"] / 8),
-                        "source": "profiles/encoder_cfg2_kernel_stats.md (rocprofv3 --pmc through bench.py)"}
-    roofline = {"kernel": f"{dom_name} (Q4_K dequant-GEMM, v_mfma_f32_16x16x32_f16)",
-                "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
-                "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6,
-                "share_of_step": dom["ms_per_step"] / sum(v["ms_per_step"] for v in kernels.values()),
-                "counters": counters}
-    if args.numerics == "hybrid" and dom_name in ("gemm_ffn_gate_up", "gemm_proj"):
-        # the hybrid FFN's products run as int8 MFMAs (two weight planes per product, so the
-        # matrix cores execute twice the algorithmic ops counted here), after the Q8_K quantizer
-        roofline.update({"kernel": f"{dom_name} (Q8_K quantize + Q4_K x Q8_K on v_mfma_i32_16x16x64_i8)",
-                         "unit": "TOP/s", "peak": PEAK_INT8_TOPS, "frac": achieved / PEAK_INT8_TOPS,
-                         "counters": None})
-
-    base = None
-    if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (ports of the reference CPU path, bounded sample) ...")
-        base = cpu_baseline(img, cfg, ids, cu, args.cpu_budget)
-        per = ", ".join(f"{k} {v['tokens_per_s']:.0f}" for k, v in base["variants"].items())
-        log(f"[bench] CPU baseline {base['value']:.1f} tokens/s on {base['cores']} threads ({per})")
-    query = None
-    if args.workload == "cfg2" and not args.no_query:
-        model.close()
-        query = run_query(args, img if args.seed == 0 else None)
-
-    line = {
-        "metric": METRIC, "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f16" if args.numerics == "default" else "f16+int8", "data": "synthetic",
-        "config": {"workload": f"{args.workload}: {desc}", "global_batch": n_seqs, "seq_len": pad,
-                   "tokens_per_step": T, "weights": "random-init N(0,0.02^2), Q4_K by the quantize tool's scale/min search (t5h_quantize_q4k); f32 embeddings and norms",
-                   "numerics": args.numerics, "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": base, "kernels": kernels,
-    }
-    if query is not None:
-        line["query"] = query
-    print(json.dumps(line), flush=True)
+    for i in range(args.queries):
+        m = models[i % len(models)]
+        m.encode_device(d_ids[i % len(d_ids)].data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+        m.synchronize()
+    for m in models:
+        m.close()
+    print(json.dumps({"counter_pass": "cfg3", "queries": args.queries, "replicas": len(models)}), flush=True)
 
 
 if __name__ == "__main__":

@@ -1,7 +1,32 @@
 // common.hpp -- shared types and helpers for the t5-hip kernels (gfx950 / CDNA4).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+namespace t5k {
+// Kernel-time events of a profiled forward (host, per thread).  While `stop` is set, the encoder's
+// launches go through hipExtLaunchKernelGGL with these events, which the runtime binds to the
+// kernel dispatch itself: start is the first such kernel's start, stop the last one's end, so
+// their elapsed time is kernel execution time inside the forward, without the gaps between
+// launches.  The launch takes `start` (once) and leaves `stop` for later launches of the class.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchTiming tl_launch_timing;
+}  // namespace t5k
+
+// hipLaunchKernelGGL, or its timed form while a profiled forward has set t5k::tl_launch_timing.
+#define T5K_LAUNCH(kernel, grid, block, shmem, stream, ...)                                          \
+  do {                                                                                             \
+    t5k::LaunchTiming& lt_ = t5k::tl_launch_timing;                                                \
+    if (lt_.stop) {                                                                                \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, lt_.start, lt_.stop, 0, __VA_ARGS__); \
+      lt_.start = nullptr;                                                                         \
+    } else {                                                                                       \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                        \
+    }                                                                                              \
+  } while (0)
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));

@@ -302,7 +302,7 @@ hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t 
   if (n_work <= 0) return hipSuccess;
   // one workgroup per work item; item b runs on XCD b % 8, and the list keeps all query tiles of
   // a (sequence, head) on one XCD so that its keys and values stay in that XCD's L2
-  hipLaunchKernelGGL(attn_relbias_kernel, dim3((unsigned)n_work), dim3(256), 0, s, a);
+  T5K_LAUNCH(attn_relbias_kernel, dim3((unsigned)n_work), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 }  // namespace t5k

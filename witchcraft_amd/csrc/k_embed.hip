@@ -138,10 +138,10 @@ hipError_t launch_embed_batch(const float* win, const int4* docs, const int* tok
   if (N <= 0) return hipSuccess;
   if (P <= 0 || P > 256 || P % 64 || stride < 0 || stride >= max_len) return hipErrorInvalidValue;
   const int nb = (N + EB_TOK - 1) / EB_TOK, step = max_len - stride;
-  hipLaunchKernelGGL(embed_flags_kernel, dim3(nb), dim3(256), 0, s, win, docs, tok_doc, N, max_len, step, P, norms,
+  T5K_LAUNCH(embed_flags_kernel, dim3(nb), dim3(256), 0, s, win, docs, tok_doc, N, max_len, step, P, norms,
                      flags, block_counts);
-  hipLaunchKernelGGL(embed_scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nb, block_offsets);
-  hipLaunchKernelGGL(embed_scatter_kernel, dim3(nb), dim3(256), 0, s, win, docs, tok_doc, N, max_len, step, P, norms,
+  T5K_LAUNCH(embed_scan_kernel, dim3(1), dim3(1024), 0, s, block_counts, nb, block_offsets);
+  T5K_LAUNCH(embed_scatter_kernel, dim3(nb), dim3(256), 0, s, win, docs, tok_doc, N, max_len, step, P, norms,
                      flags, block_offsets, out, kept_index, kept_offsets);
   return hipGetLastError();
 }

@@ -730,7 +730,7 @@ hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s
   g.tail_tiles = TMB ? (a.M - g.m_main + bmt - 1) / bmt * g.tiles_n : 0;
   const int grid = g.main_blocks + (g.tail_tiles + 7) / 8 * 8;
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<EPI, WF, MW, BN, S, TMB, HY, FMB>), dim3(grid), dim3(128 * MW), 0, s, a, g);
+  T5K_LAUNCH((gemm_kernel<EPI, WF, MW, BN, S, TMB, HY, FMB>), dim3(grid), dim3(128 * MW), 0, s, a, g);
   return hipGetLastError();
 }
 

@@ -344,11 +344,11 @@ hipError_t launch_mt(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.N / 16, (a.M + 16 * MT - 1) / (16 * MT));
   if constexpr (WIDE) {
     if (nw > 8) {
-      hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 1024>), grid, dim3(64 * nw), lds, s, a);
+      T5K_LAUNCH((gemv_kernel<EPI, WF, MT, NORM, 1024>), grid, dim3(64 * nw), lds, s, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<EPI, WF, MT, NORM, 512>), grid, dim3(64 * nw), lds, s, a);
+  T5K_LAUNCH((gemv_kernel<EPI, WF, MT, NORM, 512>), grid, dim3(64 * nw), lds, s, a);
   return hipGetLastError();
 }
 

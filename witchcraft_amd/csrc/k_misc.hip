@@ -275,7 +275,7 @@ hipError_t launch_embed(const uint32_t* ids, int T, const void* table, int fmt, 
   if (T <= 0) return hipSuccess;
   if (rec && (D > EMB_NORM_MAX_D || D % 32 || !gamma || !xn || (rec_stride != 16 && rec_stride != 64)))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err,
+  T5K_LAUNCH(embed_kernel, dim3((T + 3) / 4), dim3(256), 0, s, ids, T, table, fmt, vocab, D, x, err,
                      gamma, eps, xn, rec, rec_stride);
   return hipGetLastError();
 }
@@ -283,23 +283,23 @@ hipError_t launch_rmsnorm(const float* x, const float* w, _Float16* out, int T, 
                           hipStream_t s, float* rec, int rec_stride) {
   if (T <= 0) return hipSuccess;
   if (rec && rec_stride != 16 && rec_stride != 64) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec, rec_stride);
+  T5K_LAUNCH(rmsnorm_kernel, dim3((T + 15) / 16), dim3(256), 0, s, x, w, out, T, D, eps, rec, rec_stride);
   return hipGetLastError();
 }
 hipError_t launch_rownorm(float* y, float* norm, int T, int P, int normalize, hipStream_t s, unsigned* err) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize, err);
+  T5K_LAUNCH(rownorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, y, norm, T, P, normalize, err);
   return hipGetLastError();
 }
 hipError_t launch_f32_to_f16(const float* x, _Float16* y, size_t n, int K, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, K);
+  T5K_LAUNCH(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, K);
   return hipGetLastError();
 }
 hipError_t launch_work_list(const WorkChunk& c, int4* work, hipStream_t s) {
   if (c.n <= 0) return hipSuccess;
   if (c.n > WorkChunk::CAP) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(work_list_kernel, dim3((c.n + 255) / 256), dim3(256), 0, s, c, work);
+  T5K_LAUNCH(work_list_kernel, dim3((c.n + 255) / 256), dim3(256), 0, s, c, work);
   return hipGetLastError();
 }
 }  // namespace t5k

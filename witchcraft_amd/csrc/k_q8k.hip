@@ -160,7 +160,7 @@ hipError_t launch_q8k_quantize(const float* x, const float* gamma, float eps, in
                                hipStream_t s, int8_t* xq, float* d8, _Float16* bsop) {
   if (T <= 0) return hipSuccess;
   if (D <= 0 || D % QK_K || D > 1024 || (!out && !xq) || (xq && (!d8 || !bsop))) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(q8k_quantize_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gamma, eps, T, D, out, xq, d8, bsop);
+  T5K_LAUNCH(q8k_quantize_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gamma, eps, T, D, out, xq, d8, bsop);
   return hipGetLastError();
 }
 
@@ -168,7 +168,7 @@ hipError_t launch_q8k_operands(const uint8_t* blocks, int T, int D, int8_t* xq, 
                                hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (D <= 0 || D % QK_K || D > 1024 || !blocks || !xq || !d8 || !bsop) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(q8k_operands_kernel, dim3(T), dim3(256), 0, s, blocks, D, xq, d8, bsop);
+  T5K_LAUNCH(q8k_operands_kernel, dim3(T), dim3(256), 0, s, blocks, D, xq, d8, bsop);
   return hipGetLastError();
 }
 }  // namespace t5k

@@ -72,6 +72,10 @@ int scratch_init(int dev, void** out) {
 }
 }  // namespace
 
+namespace t5k {
+thread_local LaunchTiming tl_launch_timing;
+}
+
 namespace t5h_detail {
 // The same thread-local message for the entry points defined in other files (codec.cpp).
 int fail(int code, const std::string& msg) { return ::fail(code, msg); }
@@ -525,22 +529,32 @@ hipEvent_t take_event(t5h_model* m) {
   return e;
 }
 
+// One kernel class's launches in a profiled forward, timed by the kernels' own start/stop
+// events (t5k::tl_launch_timing, hipExtLaunchKernelGGL): from the first launch's start to the last
+// one's end, so dispatch gaps before and after are not counted and the duration is comparable
+// with a profiler's per-dispatch time of the same kernel inside the forward.
 struct Timed {
   t5h_model* m;
   int kind;
   double flops, bytes;
-  hipEvent_t a = nullptr;
-  Timed(t5h_model* m_, int k, double f, double b) : m(m_), kind(k), flops(f), bytes(b) {
+  hipEvent_t a = nullptr, b = nullptr;
+  Timed(t5h_model* m_, int k, double f, double by) : m(m_), kind(k), flops(f), bytes(by) {
     if (m->prof) {
       a = take_event(m);
-      (void)hipEventRecord(a, m->stream);
+      b = take_event(m);
+      t5k::tl_launch_timing = {a, b};
     }
   }
   ~Timed() {
-    if (!m->prof || !a) return;
-    hipEvent_t b = take_event(m);
-    (void)hipEventRecord(b, m->stream);
-    m->pending.push_back({kind, a, b, flops, bytes});
+    if (!a) return;
+    const bool launched = t5k::tl_launch_timing.start == nullptr;  // a launch took the start event
+    t5k::tl_launch_timing = {};
+    if (launched) {
+      m->pending.push_back({kind, a, b, flops, bytes});
+    } else {
+      m->event_pool.push_back(a);
+      m->event_pool.push_back(b);
+    }
   }
 };
 
