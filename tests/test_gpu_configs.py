@@ -170,6 +170,28 @@ def test_cfg4_two_lanes_bit_identical(xtr, cfg4_run):
         one.close()
 
 
+@pytest.mark.parametrize("chunk", ["8192", "1024"])
+def test_cfg4_token_chunked_ffn_bit_identical(xtr, cfg4_run, chunk):
+    """The FFN in token chunks (T5H_FFN_CHUNK; each chunk's d_ff intermediate read back by its wo
+    launch right after gate|up wrote it) gives the bits of the two whole-batch launches on the cfg4
+    batch (two lanes, chunks straddling sequence boundaries and both lanes' ends)."""
+    import os
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, _, _ = xtr
+    ids, cu, out, norms = cfg4_run
+    os.environ["T5H_FFN_CHUNK"] = chunk
+    try:
+        h = T5EncoderModel.from_gguf(img, cfg)
+    finally:
+        del os.environ["T5H_FFN_CHUNK"]
+    try:
+        got, got_n = h.encode_packed(ids, cu)
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+        assert np.array_equal(got_n.view(np.uint32), norms.view(np.uint32))
+    finally:
+        h.close()
+
+
 def test_two_lanes_with_empty_sequences(xtr):
     """The two-lane cut with empty sequences: at the front or the end of the batch (a half would
     hold no tokens, so one lane runs) and inside the second half; and a cut that would leave a

@@ -214,6 +214,7 @@ struct t5h_model {
   int gemm_mb_override = 0;  // T5H_GEMM_MB: 3 / 4 row blocks per math wave in full tiles (0 = choose)
   int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail, 3 / 4 = all thin
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
+  int ffn_chunk = 0;            // T5H_FFN_CHUNK=<tokens, multiple of 512>: FFN in token chunks
   int numerics = T5H_NUMERICS_DEFAULT;  // t5h_set_numerics
 
   // ---- weights (one device arena) ----
@@ -978,6 +979,27 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     if (rc) return rc;
   }
   const NormLink* ffn_nl = fold ? &fn : nullptr;
+  if (c.feed_forward_gated && fold && m->ffn_chunk > 0 && T > m->ffn_chunk && !use_gemv(m, T)) {
+    // The FFN in token chunks (T5H_FFN_CHUNK): each chunk's d_ff intermediate, rows [0, n) of hb,
+    // is read back by its wo launch right after gate|up wrote it, so at large batches it can stay
+    // in the MALL.  Every row is computed as in the two launches over the whole batch (bit-
+    // identical); measured no faster at cfg4.
+    for (int t0 = 0; t0 < T; t0 += m->ffn_chunk) {
+      const int n = std::min(m->ffn_chunk, T - t0);
+      NormLink f2 = fn, w2 = wn;
+      f2.rec += (size_t)t0 * 16;
+      f2.rec_next += (size_t)t0 * 16;
+      w2.rec += (size_t)t0 * 16;
+      w2.nx += tiled_index(t0, 0, D);
+      if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn + tiled_index(t0, 0, D), D, n, m->w.hb,
+                     c.d_ff, 0, nullptr, &f2)))
+        return rc;
+      if ((rc = gemm(m, K_GEMM_WO, EPI_RESID, Ly.wo, nullptr, m->w.hb, c.d_ff, n, m->w.x + (size_t)t0 * D, D, 0,
+                     nullptr, next_gamma ? &w2 : nullptr)))
+        return rc;
+    }
+    return T5H_OK;
+  }
   if (c.feed_forward_gated) {
     if ((rc = gemm(m, K_GEMM_GATE_UP, EPI_GATED, Ly.wi0, &Ly.wi1, m->w.xn, D, T, m->w.hb, c.d_ff, 0, nw1, ffn_nl)))
       return rc;
@@ -1446,6 +1468,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     if (v >= 0 && v <= 4) m->gemm_tail_override = v;
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
+  if (const char* e = getenv("T5H_FFN_CHUNK")) {
+    const int v = atoi(e);
+    if (v > 0 && v % 512 == 0) m->ffn_chunk = v;
+  }
   if (const char* e = getenv("T5H_LANES")) {
     const int v = atoi(e);
     if (v >= 2 && v <= t5h_model::MAX_LANES) m->lanes = v;
