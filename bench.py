@@ -699,12 +699,43 @@ def run_batched(args, workload: str, numerics: str, steps: int, warmup: int, cpu
         # matrix cores execute twice the algorithmic ops counted here), after the Q8_K quantizer
         roofline.update({"kernel": f"{dom_name} (Q8_K quantize + Q4_K x Q8_K on v_mfma_i32_16x16x64_i8)",
                          "unit": "TOP/s", "peak": PEAK_INT8_TOPS, "frac": achieved / PEAK_INT8_TOPS})
+    roofline["library_reference"] = library_gemm(torch, dom_name, cfg, T)
     res.update({"roofline": roofline, "kernels": kernels, "cpu_baseline": None})
     if cpu_variants and not args.no_cpu_baseline:
         log(f"[bench] {workload}: CPU baseline ({', '.join(cpu_variants)}, bounded sample) ...")
         res["cpu_baseline"] = cpu_baseline(img, cfg, ids, cu, cpu_budget, cpu_variants)
     res["_img"] = img
     return res
+
+
+def library_gemm(torch, cls: str, cfg: dict, M: int, reps: int = 20):
+    """The vendor library's plain f16 GEMM of the same shape as kernel class `cls` (M tokens):
+    torch.mm on f16 operands, which runs hipBLASLt, with no dequantization and no fused epilogue.
+    Average of `reps` back-to-back launches from HIP events on torch's current stream."""
+    D, F, inner = cfg["d_model"], cfg["d_ff"], cfg["num_heads"] * cfg["d_kv"]
+    shapes = {"gemm_ffn_gate_up": (2 * F, D), "gemm_qkv": (3 * inner, D), "gemm_o": (D, inner),
+              "gemm_ffn_wo": (D, F), "gemm_proj": (cfg["proj_dim"], D)}
+    if cls not in shapes:
+        return None
+    N, K = shapes[cls]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    a = torch.randn((M, K), device=dev, generator=g).half()
+    w_t = (torch.randn((N, K), device=dev, generator=g) * 0.02).half().t().contiguous()  # [K, N]
+    out = torch.empty((M, N), device=dev, dtype=torch.float16)
+    for _ in range(3):
+        torch.mm(a, w_t, out=out)
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        torch.mm(a, w_t, out=out)
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    return {"kernel": f"torch.mm f16 [{M},{K}] x [{K},{N}] (hipBLASLt; no dequantization, no epilogue)",
+            "avg_us": us, "tflops": tf, "frac": tf / PEAK_F16_TFLOPS}
 
 
 def summarize(args) -> None:

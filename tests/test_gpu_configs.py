@@ -192,6 +192,27 @@ def test_cfg4_token_chunked_ffn_bit_identical(xtr, cfg4_run, chunk):
         h.close()
 
 
+def test_gated_eight_math_waves_bit_identical(xtr):
+    """The gated FFN on tiles of 8 math waves x 32 tokens (T5H_GATED_MW8, the measured two-waves-
+    per-SIMD variant) gives the bits of the planner's tiles: every output keeps its K order."""
+    import os
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, gpu, _ = xtr
+    os.environ["T5H_GATED_MW8"] = "1"
+    try:
+        h = T5EncoderModel.from_gguf(img, cfg)
+    finally:
+        del os.environ["T5H_GATED_MW8"]
+    try:
+        for n, lo, hi in ((32, 32, 256), (5, 65, 300)):
+            ids, cu = synth.ragged_batch(n, lo, hi, cfg["vocab_size"], seed=BATCH_SEED + n)
+            ref, _ = gpu.encode_packed(ids, cu)
+            got, _ = h.encode_packed(ids, cu)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, lo, hi)
+    finally:
+        h.close()
+
+
 def test_two_lanes_with_empty_sequences(xtr):
     """The two-lane cut with empty sequences: at the front or the end of the batch (a half would
     hold no tokens, so one lane runs) and inside the second half; and a cut that would leave a

@@ -683,7 +683,7 @@ struct GemmGrid {
 };
 
 template <int EPI, int WF, int MW, int BN, int S, int TMB, bool HY = false, int FMB = 4>
-__global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(128 * MW) __attribute__((amdgpu_waves_per_eu(MW == 8 ? 4 : 2)))
 void gemm_kernel(GemmArgs p, GemmGrid g) {
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDSK];
   // hybrid numerics: per-row block metadata (d, dmin; mins as an MFMA operand), two blocks deep
@@ -738,6 +738,10 @@ hipError_t launch_plan(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s
 // bound by L1/TA bandwidth, not latency, and more requests in flight only add contention.
 template <int EPI, int WF, int BN>
 hipError_t launch_cfg(const t5k::GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
+  // 8 math waves of 32 tokens (two per SIMD, 128 registers each): a measurement variant of the
+  // gated FFN (T5H_GATED_MW8), same bits, not faster
+  if constexpr (EPI == EPI_GATED && WF == WF_Q4K && BN == 128)
+    if (pl.mw == 8) return launch_plan<EPI, WF, BN, 2, 8, 0, false, 2>(pl, a, s);
   if (pl.mw == 2) return launch_plan<EPI, WF, BN, 2, 2, 0>(pl, a, s);
   if (pl.mb == 3) switch (pl.tail_mb) {
       case 1: return launch_plan<EPI, WF, BN, 2, 4, 1, false, 3>(pl, a, s);
@@ -913,8 +917,12 @@ hipError_t launch_gemm_hybrid(int epi, const GemmPlan& pl, const GemmArgs& a, hi
 
 hipError_t launch_gemm(int epi, int wfmt, const GemmPlan& pl, const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  if (pl.mw != 2 && pl.mw != 4) return hipErrorInvalidValue;
-  if (pl.mb != 4 && !(pl.mb == 3 && pl.mw == 4)) return hipErrorInvalidValue;
+  if (pl.mw == 8) {  // 8 math waves of 32 tokens: gated FFN, Q4_K, 128-row tiles, full tiles only
+    if (epi != EPI_GATED || wfmt != WF_Q4K || pl.bn != 128 || pl.mb != 2 || pl.tail_mb) return hipErrorInvalidValue;
+  } else {
+    if (pl.mw != 2 && pl.mw != 4) return hipErrorInvalidValue;
+    if (pl.mb != 4 && !(pl.mb == 3 && pl.mw == 4)) return hipErrorInvalidValue;
+  }
   if (pl.tail_mb && (pl.mw != 4 || pl.m_main < 0 || pl.m_main % (64 * pl.mb) || pl.m_main >= a.M))
     return hipErrorInvalidValue;
   if (pl.bn != 64 && pl.bn != 128) return hipErrorInvalidValue;

@@ -215,6 +215,7 @@ struct t5h_model {
   int gemm_tail_override = -1;  // T5H_GEMM_TAIL: -1 = choose, 0 = full tiles only, 1 / 2 = thin tail, 3 / 4 = all thin
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
   int ffn_chunk = 0;            // T5H_FFN_CHUNK=<tokens, multiple of 512>: FFN in token chunks
+  bool gated_mw8 = false;       // T5H_GATED_MW8=1: gated FFN on 8 math waves of 32 tokens
   int numerics = T5H_NUMERICS_DEFAULT;  // t5h_set_numerics
 
   // ---- weights (one device arena) ----
@@ -719,8 +720,15 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
     return T5H_OK;
   }
   if (norm_w) return fail(T5H_ERR_INVALID, "internal: fused norm requested on the batched GEMM path");
-  const t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override,
-                                            m->gemm_bn_override, m->gemm_tail_override, m->gemm_mb_override);
+  t5k::GemmPlan plan = t5k::gemm_plan(M, W.N * (W1 ? 2 : 1), m->cus, m->gemm_mw_override, m->gemm_bn_override,
+                                      m->gemm_tail_override, m->gemm_mb_override);
+  if (epi == EPI_GATED && m->gated_mw8 && W.fmt == WF_Q4K && W.N % 64 == 0) {
+    plan.mw = 8;  // 256-token tiles of 8 math waves x 32 tokens, 128 weight rows
+    plan.mb = 2;
+    plan.bn = 128;
+    plan.m_main = M;
+    plan.tail_mb = 0;
+  }
   HIP_OK(t5k::launch_gemm(epi, W.fmt, plan, a, m->stream));
   if (m->prof) {
     ReplayRec& r = m->replay[kind];
@@ -1468,6 +1476,7 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
     if (v >= 0 && v <= 4) m->gemm_tail_override = v;
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
+  if (const char* e = getenv("T5H_GATED_MW8")) m->gated_mw8 = atoi(e) != 0;
   if (const char* e = getenv("T5H_FFN_CHUNK")) {
     const int v = atoi(e);
     if (v > 0 && v % 512 == 0) m->ffn_chunk = v;
