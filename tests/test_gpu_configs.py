@@ -192,6 +192,39 @@ def test_cfg4_token_chunked_ffn_bit_identical(xtr, cfg4_run, chunk):
         h.close()
 
 
+@pytest.mark.parametrize("layout", ["q4k", "hybrid"])
+def test_ffn_one_launch_bit_identical(xtr, xtr_hybrid, layout):
+    """The gated FFN as one launch (k_ffn.hip: h kept in LDS, wo accumulated slice by slice;
+    T5H_FFN_FUSED=1 puts every batched forward on it) gives the bits of the two launches
+    (T5H_FFN_FUSED=0): the cfg2 batch, token counts that leave a partial 64-token tile, one
+    long sequence and exact multiples of 64. The hybrid layout runs wo from f16 weights."""
+    import os
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, _, _ = xtr if layout == "q4k" else xtr_hybrid
+    hs = {}
+    try:
+        for v in ("1", "0"):
+            os.environ["T5H_FFN_FUSED"] = v
+            try:
+                hs[v] = T5EncoderModel.from_gguf(img, cfg)
+            finally:
+                del os.environ["T5H_FFN_FUSED"]
+        rng = np.random.default_rng(41)
+        batches = [synth.ragged_batch(32, 32, 256, cfg["vocab_size"], seed=BATCH_SEED)]
+        for lens in ([65], [100, 3, 200], [1000], [64] * 3, [511, 17, 1]):
+            cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+            batches.append((rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32), cu))
+        for ids, cu in batches:
+            a, an = hs["1"].encode_packed(ids, cu)
+            b, bn = hs["0"].encode_packed(ids, cu)
+            assert np.isfinite(a).all(), np.diff(cu)[:8]
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.diff(cu)[:8]
+            assert np.array_equal(an.view(np.uint32), bn.view(np.uint32)), np.diff(cu)[:8]
+    finally:
+        for h in hs.values():
+            h.close()
+
+
 def test_gated_eight_math_waves_bit_identical(xtr):
     """The gated FFN on tiles of 8 math waves x 32 tokens (T5H_GATED_MW8, the measured two-waves-
     per-SIMD variant) gives the bits of the planner's tiles: every output keeps its K order."""

@@ -230,6 +230,23 @@ hipError_t launch_matmul_t(const float* A, const float* B, float* C, int M, int 
                            hipStream_t s);
 hipError_t launch_matmul_argmax(const float* A, const float* B, uint32_t* out, int M, int N, int D, bool bf16_b,
                                 hipStream_t s);
+// The gated FFN of one block in one launch (k_ffn.hip): x += (gelu(xn' W0^T) * (xn' W1^T)) Wo^T,
+// xn' the T5LayerNorm of x folded as for the batched GEMMs, the same bits as the EPI_GATED and
+// EPI_RESID launches with their NormLinks.  D must be 768 and F % 256 == 0.
+struct FfnArgs {
+  const _Float16* xn;     // [Mpad][D] f16(x * gamma * s), operand order (the gate|up GEMM's A)
+  const void* W0;         // [F][D] Q4_K
+  const void* W1;         // [F][D] Q4_K
+  const void* Wo;         // [D][F] Q4_K or f16
+  float* x;               // [Mpad][D] residual stream, += the FFN output
+  const float* rec;       // norm records of x (the gate|up GEMM's rec)
+  float* rec_out;         // slot 15 <- the next operand scale; slots < D/64 <- sums of x^2 of the new x
+  _Float16* nx;           // the next norm's operand (may be xn), or null: no records, no operand
+  const float* ngamma;    // the next norm's weight
+  float eps;
+  int M, D, F;
+};
+hipError_t launch_ffn_fused(const FfnArgs& a, int wo_fmt, hipStream_t s);
 // Attention work items written from kernel arguments: CAP sequences per launch.
 // Attention work list entries passed by value: item q of entry i is written at
 // work[pos + 8 q] as (start, len, 64 q, head); an entry of length 0 writes `start` empty items.

@@ -120,11 +120,11 @@ struct PendingTiming {
 
 enum KernelKind {
   K_EMBED, K_RMSNORM, K_GEMM_QKV, K_ATTN, K_GEMM_O, K_GEMM_GATE_UP, K_GEMM_WO, K_GEMM_PROJ,
-  K_ROWNORM, K_COUNT
+  K_ROWNORM, K_FFN, K_COUNT
 };
 const char* const kKernelNames[K_COUNT] = {
     "embed_gather", "rmsnorm", "gemm_qkv", "attention", "gemm_o", "gemm_ffn_gate_up",
-    "gemm_ffn_wo", "gemm_proj", "rownorm"};
+    "gemm_ffn_wo", "gemm_proj", "rownorm", "ffn_fused"};
 
 // Per-forward device buffers, rows padded to tpad = roundup(T, 512) + 128.
 struct Workspace {
@@ -148,7 +148,7 @@ struct Workspace {
 // The arguments of the last launch of each kernel class in a profiled forward, so that
 // t5h_replay_kernel can relaunch it back to back between two events.
 struct ReplayRec {
-  enum Type { NONE, GEMM, GEMV, ATTN, EMBED, ROWNORM, RMSNORM, HYBRID } type = NONE;
+  enum Type { NONE, GEMM, GEMV, ATTN, EMBED, ROWNORM, RMSNORM, HYBRID, FFN } type = NONE;
   int epi = 0, wfmt = 0, n = 0;
   GemmArgs ga{};
   t5k::GemmPlan plan{};
@@ -168,6 +168,8 @@ struct ReplayRec {
   // eps, n (tokens), D for the quantizer; ga / plan for the GEMM (epi: EPI_GATED or EPI_F32)
   float* hd8 = nullptr;
   _Float16* hbs = nullptr;
+  // one-launch FFN (wfmt: Wo's format)
+  t5k::FfnArgs fa{};
 };
 
 struct StagingSlot {
@@ -216,6 +218,9 @@ struct t5h_model {
   bool fold_norm_off = false;   // T5H_FOLD_NORM=0: standalone RMSNorm launches on the batched path
   int ffn_chunk = 0;            // T5H_FFN_CHUNK=<tokens, multiple of 512>: FFN in token chunks
   bool gated_mw8 = false;       // T5H_GATED_MW8=1: gated FFN on 8 math waves of 32 tokens
+  // T5H_FFN_FUSED=<tokens>: batches (lane parts) of at least that many tokens run the gated FFN
+  // as one launch (k_ffn.hip), bit-identical to the two launches and measured slower; 0 = off.
+  int ffn_fused_min = 0;
   int numerics = T5H_NUMERICS_DEFAULT;  // t5h_set_numerics
 
   // ---- weights (one device arena) ----
@@ -613,6 +618,15 @@ const Layer& layer_w(const t5h_model* m, int l) {
 
 // Every norm folded.  With hybrid numerics the FFN's and the projection's Q8_K quantizer
 // normalises its own f32 input, so only the attention norm is folded there.
+// The one-launch gated FFN (k_ffn.hip) for this layer and batch: batched path, default numerics,
+// d_model 768, Q4_K wi_0 / wi_1 and a Q4_K or f16 wo, at least ffn_fused_min tokens.
+bool use_ffn_fused(const t5h_model* m, const Layer& Ly, int T) {
+  const t5h_config& c = m->cfg;
+  return m->ffn_fused_min > 0 && T >= m->ffn_fused_min && m->ffn_chunk == 0 && !use_gemv(m, T) &&
+         m->numerics == T5H_NUMERICS_DEFAULT && c.d_model == 768 && c.d_ff % 256 == 0 && Ly.wi0.fmt == WF_Q4K &&
+         Ly.wi1.fmt == WF_Q4K && (Ly.wo.fmt == WF_Q4K || Ly.wo.fmt == WF_F16);
+}
+
 bool fold_norm(const t5h_model* m, int T) {
   return fold_attn_norm(m, T) && m->numerics == T5H_NUMERICS_DEFAULT;
 }
@@ -987,6 +1001,36 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     if (rc) return rc;
   }
   const NormLink* ffn_nl = fold ? &fn : nullptr;
+  if (c.feed_forward_gated && fold && use_ffn_fused(m, Ly, T)) {
+    // gate|up, gelu * up and wo in one launch, h never leaving the CU (k_ffn.hip); the same bits
+    // as the two launches below
+    if (fn.rec_next != wn.rec) return fail(T5H_ERR_INVALID, "internal: FFN norm records out of step");
+    t5k::FfnArgs fa{};
+    fa.xn = m->w.xn;
+    fa.W0 = Ly.wi0.w;
+    fa.W1 = Ly.wi1.w;
+    fa.Wo = Ly.wo.w;
+    fa.x = m->w.x;
+    fa.rec = fn.rec;
+    fa.rec_out = fn.rec_next;
+    fa.nx = next_gamma ? wn.nx : nullptr;
+    fa.ngamma = next_gamma;
+    fa.eps = c.layer_norm_epsilon;
+    fa.M = T;
+    fa.D = D;
+    fa.F = c.d_ff;
+    const double flops = 6.0 * T * D * c.d_ff;
+    const double bytes = (double)(Ly.wi0.bytes() + Ly.wi1.bytes() + Ly.wo.bytes()) + 2.0 * T * D + 8.0 * T * D;
+    Timed t(m, K_FFN, flops, bytes);
+    HIP_OK(t5k::launch_ffn_fused(fa, Ly.wo.fmt, m->stream));
+    if (m->prof) {
+      ReplayRec& r = m->replay[K_FFN];
+      r.type = ReplayRec::FFN;
+      r.fa = fa;
+      r.wfmt = Ly.wo.fmt;
+    }
+    return T5H_OK;
+  }
   if (c.feed_forward_gated && fold && m->ffn_chunk > 0 && T > m->ffn_chunk && !use_gemv(m, T)) {
     // The FFN in token chunks (T5H_FFN_CHUNK): each chunk's d_ff intermediate, rows [0, n) of hb,
     // is read back by its wo launch right after gate|up wrote it, so at large batches it can stay
@@ -1477,6 +1521,10 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   }
   if (const char* e = getenv("T5H_FOLD_NORM")) m->fold_norm_off = atoi(e) == 0;
   if (const char* e = getenv("T5H_GATED_MW8")) m->gated_mw8 = atoi(e) != 0;
+  if (const char* e = getenv("T5H_FFN_FUSED")) {
+    const int v = atoi(e);
+    m->ffn_fused_min = v > 0 ? v : 0;
+  }
   if (const char* e = getenv("T5H_FFN_CHUNK")) {
     const int v = atoi(e);
     if (v > 0 && v % 512 == 0) m->ffn_chunk = v;
@@ -2017,6 +2065,7 @@ int t5h_replay_kernel(t5h_model* m, int32_t kind, int32_t reps, double* avg_us) 
       case ReplayRec::GEMM: return t5k::launch_gemm(r.epi, r.wfmt, r.plan, r.ga, m->stream);
       case ReplayRec::GEMV: return t5k::launch_gemv(r.epi, r.wfmt, r.ga, m->stream);
       case ReplayRec::ATTN: return t5k::launch_attention(r.aa, r.n, r.D, m->stream);
+      case ReplayRec::FFN: return t5k::launch_ffn_fused(r.fa, r.wfmt, m->stream);
       case ReplayRec::EMBED:
         return t5k::launch_embed(r.ids, r.n, r.table, r.fmt, r.vocab, r.D, r.x, m->err_flag, m->stream, r.gamma,
                                  r.eps, r.xn, r.rec, r.rec_stride);
