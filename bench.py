@@ -613,11 +613,13 @@ NUMERICS = {"default": 0, "hybrid": 1, "hybrid_bf16": 2}
 
 
 def run_batched(args, workload: str, numerics: str, steps: int, warmup: int, cpu_variants=None,
-                cpu_budget: float = 0.0, img: bytes | None = None) -> dict:
+                cpu_budget: float = 0.0, img: bytes | None = None, ffn_one_launch: bool = False) -> dict:
     """One batched workload (cfg2 / cfg4 / cfg5): `warmup` untimed forwards, then `steps` forwards
     timed from the host between device synchronisations (whole-job tokens/s, ids resident in
     HBM), then the per-class in-forward kernel table, the dominant GEMM class against its
-    matrix-core roofline, and the CPU baseline on a bounded sample (cpu_variants, or none)."""
+    matrix-core roofline, and the CPU baseline on a bounded sample (cpu_variants, or none).
+    ffn_one_launch: also time the same batch with the gated FFN as one launch that keeps the d_ff
+    intermediate on chip (T5H_FFN_FUSED; bit-identical, not the default) next to the two launches."""
     import torch
 
     from witchcraft_amd import synth
@@ -701,11 +703,56 @@ def run_batched(args, workload: str, numerics: str, steps: int, warmup: int, cpu
                          "unit": "TOP/s", "peak": PEAK_INT8_TOPS, "frac": achieved / PEAK_INT8_TOPS})
     roofline["library_reference"] = library_gemm(torch, dom_name, cfg, T)
     res.update({"roofline": roofline, "kernels": kernels, "cpu_baseline": None})
+    if ffn_one_launch and numerics == "default":
+        res["ffn_one_launch"] = ffn_one_launch_leg(img, cfg, cu, d_ids, d_out, d_norm, kernels, T)
     if cpu_variants and not args.no_cpu_baseline:
         log(f"[bench] {workload}: CPU baseline ({', '.join(cpu_variants)}, bounded sample) ...")
         res["cpu_baseline"] = cpu_baseline(img, cfg, ids, cu, cpu_budget, cpu_variants)
     res["_img"] = img
     return res
+
+
+def ffn_one_launch_leg(img: bytes, cfg: dict, cu, d_ids, d_out, d_norm, kernels: dict, T: int,
+                       steps: int = 5) -> dict:
+    """The gated FFN as one launch per layer (k_ffn.hip: 64-token tiles, h kept in LDS, never
+    written to memory; the same bits as the two launches), on a second handle created with
+    T5H_FFN_FUSED=1: whole-step time over `steps` forwards and its in-forward kernel time, next to
+    the default two launches (gate|up + wo) of the same batch from `kernels`."""
+    import torch
+
+    from witchcraft_amd.encoder import T5EncoderModel
+
+    os.environ["T5H_FFN_FUSED"] = "1"
+    try:
+        fm = T5EncoderModel.from_gguf(img, cfg, hip_device=0)
+    finally:
+        del os.environ["T5H_FFN_FUSED"]
+    try:
+        def step():
+            fm.encode_device(d_ids.data_ptr(), cu, d_out.data_ptr(), d_norm.data_ptr())
+
+        for _ in range(2):
+            step()
+        fm.synchronize()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            step()
+        fm.synchronize()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t) / steps * 1e3
+        fk = kernel_table(fm, step, 3).get("ffn_fused")
+    finally:
+        fm.close()
+    two = sum(kernels[k]["avg_us"] for k in ("gemm_ffn_gate_up", "gemm_ffn_wo") if k in kernels)
+    out = {"kernel": "ffn_fused_kernel (one launch per layer, d_ff intermediate in LDS, bit-identical; "
+                     "opt-in T5H_FFN_FUSED)",
+           "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "two_launch_avg_us": two}
+    if fk:
+        out.update({"avg_us": fk["avg_us"], "tflops": fk.get("tflops"), "frac": fk.get("mfma_frac")})
+    log(f"[bench] one-launch FFN: {ms:.3f} ms/step; ffn_fused {out.get('avg_us', float('nan')):.1f} us "
+        f"vs gate|up + wo {two:.1f} us per layer (one lane)")
+    return out
 
 
 def library_gemm(torch, cls: str, cfg: dict, M: int, reps: int = 20):
@@ -764,7 +811,8 @@ def summarize(args) -> None:
                     "1": "resid"}.get(m.group(2))
         for key, cls in (("embed_kernel", "embed_gather"), ("rownorm_kernel", "rownorm"),
                          ("rmsnorm_kernel", "rmsnorm"), ("attn_relbias_kernel", "attention"),
-                         ("q8k_quantize_kernel", "q8k_quantize"), ("copyBuffer", "copy")):
+                         ("q8k_quantize_kernel", "q8k_quantize"), ("ffn_fused_kernel", "ffn_fused"),
+                         ("copyBuffer", "copy")):
             if key in name:
                 return key if cls is None else cls
         return None
@@ -938,7 +986,7 @@ def main() -> None:
         # steps), with its dominant GEMM's in-forward roofline and a small CPU sample.
         extra = {}
         budget = min(args.cpu_budget, 4.0)
-        r4 = run_batched(args, "cfg4", "default", 10, 3, ("f32_torch",), budget)
+        r4 = run_batched(args, "cfg4", "default", 10, 3, ("f32_torch",), budget, ffn_one_launch=True)
         r4.pop("_img")
         extra["cfg4"] = r4
         img5 = None
