@@ -726,6 +726,48 @@ def test_small_multi_sequence_batches_vs_oracle(xtr, lens):
     assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
 
 
+def test_two_handles_on_two_threads(enc_mod, xtr):
+    """Two handles used from two threads at the same time, as the reference's indexer and search
+    threads each own an Embedder (src/napi.rs:293,483): every result of either thread equals the
+    single-threaded result bit for bit (query-sized, small and cfg2-sized batches, interleaved in
+    opposite orders so that different shapes overlap)."""
+    import threading
+    cfg, img, gpu, _ = xtr
+    other = enc_mod.T5EncoderModel.from_gguf(img, cfg)
+    try:
+        rng = np.random.default_rng(77)
+        batches = []
+        for lens in ([32], [200, 311, 97], [17, 5, 40]):
+            cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+            batches.append((rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32), cu))
+        batches.append(synth.ragged_batch(32, 32, 256, cfg["vocab_size"], seed=1000))
+        refs = [gpu.encode_packed(ids, cu) for ids, cu in batches]
+        errors = []
+
+        def work(h, order):
+            try:
+                for it in range(6):
+                    for b in order:
+                        ids, cu = batches[b]
+                        out, norms = h.encode_packed(ids, cu)
+                        if not (np.array_equal(out.view(np.uint32), refs[b][0].view(np.uint32))
+                                and np.array_equal(norms.view(np.uint32), refs[b][1].view(np.uint32))):
+                            errors.append((b, it))
+            except Exception as e:  # reported below, on the test's thread
+                errors.append(repr(e))
+
+        ts = [threading.Thread(target=work, args=(gpu, [0, 1, 2, 3])),
+              threading.Thread(target=work, args=(other, [3, 2, 1, 0]))]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in ts), "a thread did not finish"
+        assert not errors, errors[:5]
+    finally:
+        other.close()
+
+
 def test_two_handles_device_encodes_back_to_back(enc_mod, xtr):
     """Two handles enqueue device encodes on their own streams without waiting for each other;
     each result equals the synchronous result bit for bit."""
