@@ -756,8 +756,8 @@ def test_two_handles_on_two_threads(enc_mod, xtr):
             except Exception as e:  # reported below, on the test's thread
                 errors.append(repr(e))
 
-        ts = [threading.Thread(target=work, args=(gpu, [0, 1, 2, 3])),
-              threading.Thread(target=work, args=(other, [3, 2, 1, 0]))]
+        ts = [threading.Thread(target=work, args=(gpu, [0, 1, 2, 3]), daemon=True),
+              threading.Thread(target=work, args=(other, [3, 2, 1, 0]), daemon=True)]
         for t in ts:
             t.start()
         for t in ts:
