@@ -616,8 +616,6 @@ const Layer& layer_w(const t5h_model* m, int l) {
   return m->numerics == T5H_NUMERICS_HYBRID_BF16 ? m->layers_bf[l] : m->layers[l];
 }
 
-// Every norm folded.  With hybrid numerics the FFN's and the projection's Q8_K quantizer
-// normalises its own f32 input, so only the attention norm is folded there.
 // The one-launch gated FFN (k_ffn.hip) for this layer and batch: batched path, default numerics,
 // d_model 768, Q4_K wi_0 / wi_1 and a Q4_K or f16 wo, at least ffn_fused_min tokens.
 bool use_ffn_fused(const t5h_model* m, const Layer& Ly, int T) {
@@ -627,6 +625,8 @@ bool use_ffn_fused(const t5h_model* m, const Layer& Ly, int T) {
          Ly.wi1.fmt == WF_Q4K && (Ly.wo.fmt == WF_Q4K || Ly.wo.fmt == WF_F16);
 }
 
+// Every norm folded.  With hybrid numerics the FFN's and the projection's Q8_K quantizer
+// normalises its own f32 input, so only the attention norm is folded there.
 bool fold_norm(const t5h_model* m, int T) {
   return fold_attn_norm(m, T) && m->numerics == T5H_NUMERICS_DEFAULT;
 }
