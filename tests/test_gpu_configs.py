@@ -225,6 +225,32 @@ def test_ffn_one_launch_bit_identical(xtr, xtr_hybrid, layout):
             h.close()
 
 
+def test_ffn_one_launch_cfg4_two_lanes_and_layers(xtr, cfg4_run):
+    """The one-launch FFN on the full cfg4 batch (two lanes of ~35k tokens, 555 tiles each) gives
+    the default handle's bits, and so does a teacher-forced block through t5h_layer_forward
+    (one lane, a partial last tile)."""
+    import os
+    from witchcraft_amd.encoder import T5EncoderModel
+    cfg, img, gpu, _ = xtr
+    ids, cu, out, norms = cfg4_run
+    os.environ["T5H_FFN_FUSED"] = "1"
+    try:
+        h = T5EncoderModel.from_gguf(img, cfg)
+    finally:
+        del os.environ["T5H_FFN_FUSED"]
+    try:
+        got, got_n = h.encode_packed(ids, cu)
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+        assert np.array_equal(got_n.view(np.uint32), norms.view(np.uint32))
+        x = np.random.default_rng(43).standard_normal((777, cfg["d_model"])).astype(np.float32)
+        lcu = np.array([0, 300, 777], np.int32)
+        for layer in (0, 11):
+            assert np.array_equal(h.layer_forward(layer, x, lcu).view(np.uint32),
+                                  gpu.layer_forward(layer, x, lcu).view(np.uint32)), layer
+    finally:
+        h.close()
+
+
 def test_gated_eight_math_waves_bit_identical(xtr):
     """The gated FFN on tiles of 8 math waves x 32 tokens (T5H_GATED_MW8, the measured two-waves-
     per-SIMD variant) gives the bits of the planner's tiles: every output keeps its K order."""
