@@ -7,7 +7,7 @@ import pytest
 
 from witchcraft_amd.encoder import attention_work
 
-QT = 64  # queries per workgroup
+QT = 128  # queries per workgroup
 
 
 def _check(cu, heads, max_len=2048):

@@ -122,8 +122,8 @@ __host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
   return s;
 }
 
-// Queries per attention workgroup (one work list item): 4 waves x 16.
-constexpr int ATTN_QT = 64;
+// Queries per attention workgroup (one work list item): 4 waves x 32.
+constexpr int ATTN_QT = 128;
 
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]

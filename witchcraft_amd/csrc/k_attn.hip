@@ -8,289 +8,316 @@
 // (:452-483), so it is read from a per-head LUT indexed by the signed distance instead of
 // materialising [H, L, L].
 //
-// Workgroup = 4 wave64s = 64 queries of one (sequence, head); each wave owns 16 queries.
-// Keys are streamed in tiles of 64 through double-buffered LDS with an online softmax.  The
-// tiles travel global -> LDS without registers (global_load_lds_dwordx4): K and V rows as
-// they lie in memory, 128 B per key, and the bias values a tile needs (by j - i).  The next
-// tile's loads are issued before the current tile is computed; one barrier per tile.
+// Workgroup = 4 wave64s = 128 queries of one (sequence, head); each wave owns 32 queries and
+// runs v_mfma_f32_32x32x16_f16, so every K and V operand it reads from LDS feeds 32 queries.
+// Keys are streamed in tiles of 64 through a three-deep LDS ring with an online softmax.  The
+// tiles travel global -> LDS without registers (global_load_lds_dwordx4): K and V rows as they
+// lie in memory, 128 B per key, and the bias values a tile needs (by j - i).  A tile's loads
+// are issued two tiles ahead; one barrier per tile.
 //
-// The score block is computed transposed, S^T = K . Q^T, so that the accumulator layout
-// (lane = query column, 4 consecutive keys per lane group) is exactly the B-operand layout of
-// O^T = V^T . P^T: P never leaves registers.  The V^T operand (8 keys of one dim per lane) is
-// read from the row-major V tile with ds_read_b64_tr_b16, which hands lane n of each 16-lane
-// group column n of a 4-row block, so V needs no transpose on its way in.
+// The score block is computed transposed, S^T = K . Q^T (32 keys x 32 queries per MFMA), so
+// that the accumulator layout (lane = query column; lane half h holds keys 8a + 4h + b) is, four
+// registers at a time, the B operand of O^T = V^T . P^T with the keys of each 16-key step taken
+// in the order {4h .. 4h+3, 8+4h .. 8+4h+3}: P never leaves registers.  The V^T operand (32 dims
+// x those 8 keys per lane) is read from the row-major V tile with ds_read_b64_tr_b16, which
+// hands lane n of each 16-lane group column n of a 4-row block, so V needs no transpose on its
+// way in.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
 
-constexpr int QT = ATTN_QT;  // queries per workgroup
-constexpr int KT = 64;   // keys per tile
-constexpr int DK = 64;   // head dim (d_kv)
+constexpr int QT = ATTN_QT;     // queries per workgroup
+constexpr int QW = 32;          // queries per wave
+constexpr int NWV = QT / QW;    // waves per workgroup
+constexpr int KT = 64;          // keys per tile
+constexpr int DK = 64;          // head dim (d_kv)
+constexpr int BSN = 64 * NWV;   // bias values staged per tile (QT + KT - 1 of them are read)
+constexpr int LOADS = 5;        // global -> LDS loads per wave per tile: 2 K, 2 V, 1 bias
 constexpr float LOG2E = 1.4426950408889634f;
+static_assert(NWV == 4 && 16 * NWV == KT && BSN >= QT + KT, "tile shape");
 
 typedef short s4v __attribute__((ext_vector_type(4)));
 
-// LDS tiles are 64 keys x 64 dims of f16 in the swz64 layout (128 B rows, XOR-swizzled
-// 16-byte chunks): the K operand reads and the transposed V reads are conflict-free.
-__device__ __forceinline__ int swz(int row, int col) { return swz64(row, col); }
+// One slot of the LDS ring: a key tile's K and V rows and its bias values.
+struct __attribute__((aligned(16))) Slot {
+  _Float16 k[KT * DK], v[KT * DK];
+  float b[BSN];
+};
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// LDS tiles are 64 keys x 64 dims of f16, 128 B rows of eight 16-byte chunks; chunk c of row r
+// sits at position c ^ rot(r), rot(r) = r's low three bits with bits 1 and 2 swapped.  The
+// rotation is a bijection on each 8 rows, so the K operand reads (8 rows x one chunk per 8
+// lanes) are conflict-free, and it sends rows r and r + 2 to opposite 64-byte halves of a row, so
+// a transposed V read (per 32 lanes 4 consecutive rows x 4 chunks, 256 B over the 64 banks,
+// where rows r and r + 2 share bank offsets) is conflict-free as well; the plain r % 8 rotation
+// gives 2-way conflicts there.
+__device__ __forceinline__ int rot(int row) { return (row & 1) | ((row & 2) << 1) | ((row & 4) >> 1); }
+__device__ __forceinline__ int swz(int row, int col) { return row * DK + ((((col >> 3) ^ rot(row)) & 7) << 3) + (col & 7); }
+
+// Global -> LDS loads (global_load_lds), written as inline asm so that the compiler does not
+// track them: its tracking waits for every outstanding one before a read of one of the ring
+// slots (it cannot tell the slots apart there), which would stall on the tile just issued.
+// The kernel orders them itself: a wave issues exactly LOADS of them per tile and waits with
+// vmcnt before the barrier that publishes the tile; the "memory" clobbers keep every LDS
+// access on its side of these statements.  M0 holds the wave's LDS destination; the 16-byte
+// form writes lane l's 16 bytes at M0 + 16 l, the 4-byte form lane l's 4 bytes at M0 + 4 l.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_load16(const void* src, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(const void* src, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
 
 // Global -> LDS copy of one 64-row tile by this wave's 16 rows: LDS slot l of an instruction
-// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ (row % 8), so
+// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ rot(row), so
 // each group of 8 lanes still reads one 128-byte row.  Rows at or past `nrows` repeat the last
 // row of the sequence: finite values, which the masked scores (P = 0) then ignore.
 __device__ __forceinline__ void dma_tile(const _Float16* src, int nrows, _Float16* dst, int wave, int lane) {
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int row = 16 * wave + 8 * j + (lane >> 3);
-    const int chunk = (lane ^ row) & 7;
+    const int chunk = (lane ^ rot(row)) & 7;
     const int srow = row < nrows ? row : nrows - 1;
-    __builtin_amdgcn_global_load_lds(src + (size_t)srow * DK + chunk * 8, dst + (16 * wave + 8 * j) * DK, 16, 0, 0);
+    lds_load16(src + (size_t)srow * DK + chunk * 8, lds_offset(dst + (16 * wave + 8 * j) * DK));
   }
 }
 
-// The V^T operand of P.V step ks for dims 16 db..16 db+15: lane (n, g) = (lane % 16, lane / 16)
-// gets V[32 ks + 4 g + r][16 db + n] and V[32 ks + 16 + 4 g + r][16 db + n], r = 0..3 -- the
-// keys of K-slots 8g..8g+7 of the P^T operand.  Lane i of a 16-lane group addresses row
-// base + i / 4, dims 16 db + 4 (i % 4): the transposing read returns column n of those 4 rows.
-__device__ __forceinline__ h8 v_operand(const _Float16* Vb, int ks, int db, int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const int row = 32 * ks + 4 * g + (i >> 2), col = 16 * db + 4 * (i & 3);
+// Per-lane LDS offsets (f16 elements from a tile's base) of the operand reads.
+// k[ds]: the K operand of dims 16 ds .. +15 for key half 0 (key row l % 32, dims + 8 (l / 32));
+// half kb adds 32 rows.  v[db]: the V^T operand of dims 32 db .. +31 for key step 0 (below);
+// step c adds 16 rows, its second 8 keys another 8.  Rows that differ by a multiple of 8 share
+// their rotation, so those additions are constants that fold into the reads' immediate offsets.
+struct LaneOfs {
+  int k[4], v[2];
+};
+__device__ __forceinline__ LaneOfs lane_offsets(int lane) {
+  const int l32 = lane & 31, h = lane >> 5, i = lane & 15, g = lane >> 4;
+  LaneOfs o;
+#pragma unroll
+  for (int ds = 0; ds < 4; ds++) o.k[ds] = swz(l32, 16 * ds + 8 * h);
+#pragma unroll
+  for (int db = 0; db < 2; db++) o.v[db] = swz(4 * h + (i >> 2), 32 * db + 16 * (g & 1) + 4 * (i & 3));
+  return o;
+}
+
+// The V^T operand of P.V key step c (keys 16c .. 16c+15 of the tile) for dims 32 db .. +31 (vo =
+// LaneOfs::v[db]): lane l gets dim 32 db + l % 32 of the keys 16c + 4h + r and 16c + 8 + 4h + r,
+// r = 0..3, h = l / 32 -- the order in which the lane's P^T operand holds them.  Within a
+// 16-lane group, lane i addresses row 16c + 4h + i / 4, dims c0 + 4 (i % 4); the transposing
+// read returns column c0 + n of those 4 rows to lane n.
+__device__ __forceinline__ h8 v_operand(const _Float16* Vb, int c, int vo) {
   typedef __attribute__((address_space(3))) s4v lds_s4;
-  const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vb + swz(row, col)));
-  const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vb + swz(row + 16, col)));
+  const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vb + vo + 16 * c * DK));
+  const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vb + vo + (16 * c + 8) * DK));
   h8 r;
   __builtin_memcpy(&r, &lo, 8);
   __builtin_memcpy(reinterpret_cast<char*>(&r) + 8, &hi, 8);
   return r;
 }
 
-// P = 2^(S log2e + mb) of this tile's valid key blocks into the f16 P^T operand; returns this
-// lane's sum of P.  K-slots 8lg..8lg+7 of step ks are keys {32ks + 4lg + 0..3, 32ks + 16 + 4lg + 0..3}.
-template <int NKB>
-__device__ __forceinline__ float tile_exp(const f4 (&s)[4], float mb, h8 (&pb)[2]) {
-  float rs = 0.f;
-#pragma unroll
-  for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float e = 0.f;
-      if (kb < NKB) {
-        e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], LOG2E, mb));
-        rs += e;
-      }
-      pb[kb >> 1][(kb & 1) * 4 + i] = (_Float16)e;
-    }
-  return rs;
-}
-
-// One key tile of one wave's 16 queries: S^T = K . Q^T, bias, softmax against the running
+// One key tile of one wave's 32 queries: S^T = K . Q^T + bias, softmax against the running
 // reference max m_run, O^T += V^T . P^T.
-// NKB = 16-key blocks of the tile that hold keys < L (the rest are skipped: their P is 0);
-// MASK: the tile holds keys >= L, which get score -inf (only a sequence's last tile);
-// FIRST: the sequence's first tile, which sets the reference max.
+// FULL: both 32-key halves of the tile hold keys < L; otherwise only the first does, and the
+// second is skipped (its P is 0).  MASK: the tile holds keys >= L, which get score -inf (a
+// sequence's last tile).
 //
-// The reference max moves only when needed: P is first taken against the current m_run, and
-// only if some lane's sum of P exceeds 2^14 (so that a P could leave the f16 range, and on the
-// first tile, where m_run = -inf gives inf) is the tile's true max taken, O and l rescaled and P
-// recomputed.  Same result up to rounding: P and l carry the same factor 2^((m - m_run) log2e),
-// divided out at the end, and m_run is a score already seen, so l >= 1.  l is kept per lane
-// (this lane's keys) and reduced across the four lanes of a query only at the end.
-//
-// FAR: every (query, key) distance of the tile lies where the bias buckets have saturated, so
-// the bias is the single value cb: it joins the exponent's constant instead of the scores.
-template <int NKB, bool MASK, bool FIRST, bool FAR>
+// The reference max moves only when needed.  A query's scores lie in two lanes (the two key
+// halves of each 8-key group), so its tile max is one permlane32 swap away; the reference
+// m_run is moved to the running max, and O and l rescaled, only when some query's tile max
+// exceeds m_run by more than 14 / log2(e) (always on the first tile, where m_run = -inf), so
+// every P = 2^((s - m_run) log2e) stays at most 2^14, well inside f16.  Same result up to
+// rounding: P and l carry the same factor, divided out at the end, and m_run is a score
+// already seen, so l >= 1.  A rescale on every tile measured slower.  l sums the f16 P that the
+// P.V product uses; it is kept per lane (this lane's keys) and reduced across the two lanes of
+// a query only at the end.
+template <bool FULL, bool MASK>
 __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* Vb, const float* Bsb, int bofs,
-                                          float cb, const h8 (&qf)[2], int k0, int L, float& m_run,
-                                          float& l_run, f4 (&o)[4]) {
-  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-  if (!FAR) cb = 0.f;
-  // S^T[key][query] (+ bias for the valid key blocks of 16 unless FAR): the accumulators start
-  // from the bias, so the matrix core does the add.  Independent accumulators back to back: no
-  // MFMA waits on the one before it.
-  f4 s[4];
+                                          LaneOfs lo, const h8 (&qf)[4], int k0, int L, float& m_run,
+                                          float& l_run, f16v (&o)[2]) {
+  constexpr int NS = FULL ? 2 : 1;  // 32-key halves with keys < L
+  const int h = (threadIdx.x >> 5) & 1;
+  // The offsets pass through an empty asm, so the compiler keeps these eight lane values and
+  // folds each ring slot's base into the reads' immediate offsets, rather than holding a
+  // precomputed address per slot.
+  asm volatile("" : "+v"(bofs), "+v"(lo.k[0]), "+v"(lo.k[1]), "+v"(lo.k[2]), "+v"(lo.k[3]), "+v"(lo.v[0]),
+               "+v"(lo.v[1]));
+  // S^T[key][query] + bias: register r of half kb holds key 32 kb + 8 (r / 4) + 4 h + r % 4.
+  // The accumulators start from the bias, so the matrix core does the add.
+  f16v s[NS];
 #pragma unroll
-  for (int kb = 0; kb < 4; kb++) {
-    s[kb] = f4{0.f, 0.f, 0.f, 0.f};
-    if (!FAR && kb < NKB)
+  for (int kb = 0; kb < NS; kb++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) s[kb][i] = Bsb[bofs + kb * 16 + i];
-  }
+    for (int r = 0; r < 16; r++) s[kb][r] = Bsb[bofs + 32 * kb + 8 * (r >> 2) + (r & 3)];
+  // every LDS operand of the tile is read before the products that use it: the K operands
+  // ahead of the score products, the V^T operands ahead of the softmax, whose VALU work covers
+  // their latency
+  h8 ka[4][NS];
 #pragma unroll
-  for (int ds = 0; ds < 2; ds++)
+  for (int ds = 0; ds < 4; ds++)
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-      const h8 a = *reinterpret_cast<const h8*>(&Ksb[swz(kb * 16 + lr, ds * 32 + lg * 8)]);
-      s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
-    }
+    for (int kb = 0; kb < NS; kb++) ka[ds][kb] = *reinterpret_cast<const h8*>(&Ksb[lo.k[ds] + 32 * kb * DK]);
+#pragma unroll
+  for (int ds = 0; ds < 4; ds++)
+#pragma unroll
+    for (int kb = 0; kb < NS; kb++) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ds][kb], qf[ds], s[kb], 0, 0, 0);
+  h8 va[2 * NS][2];
+#pragma unroll
+  for (int c = 0; c < 2 * NS; c++)
+#pragma unroll
+    for (int db = 0; db < 2; db++) va[c][db] = v_operand(Vb, c, lo.v[db]);
   if (MASK) {
+    const int lim = L - k0 - 4 * h;  // key 32 kb + 8 (r / 4) + 4 h + r % 4 >= L - k0
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++)
+    for (int kb = 0; kb < NS; kb++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (k0 + kb * 16 + lg * 4 + i >= L) s[kb][i] = -INFINITY;
+      for (int r = 0; r < 16; r++)
+        if (32 * kb + 8 * (r >> 2) + (r & 3) >= lim) s[kb][r] = -INFINITY;
   }
-  h8 pb[2];
-  float rs = 0.f, corr = 1.f;
-  if (!FIRST) rs = tile_exp<NKB>(s, (cb - m_run) * LOG2E, pb);
-  // !(rs <= 2^14) also catches NaN
-  const bool remax = FIRST || __any(!(rs <= 16384.f));
-  if (remax) {
-    float mx = -INFINITY;
+  float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++)
+  for (int kb = 0; kb < NS; kb++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kb][i]);
-    mx = max_xor32(max_xor16(mx)) + cb;  // finite: key k0 < L is valid
+    for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
+  mx = max_xor32(mx);  // finite: key k0 < L is valid
+  if (__any(!((mx - m_run) * LOG2E <= 14.f))) {  // !(x <= 14) also catches NaN
+    // the rescale of O sits in a branch of its own, so the accumulators keep their registers
     const float m_new = fmaxf(m_run, mx);
-    if (!FIRST) corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);  // 1 where the max did not move
+    // 1 where the max did not move, 0 on the first tile (O and l are still 0 there)
+    const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
     m_run = m_new;
-    rs = tile_exp<NKB>(s, (cb - m_new) * LOG2E, pb);
-  }
-  // the rescale of O sits in a branch of its own, so the accumulators keep their registers
-  if (!FIRST && remax) {
     l_run *= corr;
 #pragma unroll
-    for (int db = 0; db < 4; db++) o[db] *= corr;
+    for (int db = 0; db < 2; db++) o[db] *= corr;
   }
-  l_run += rs;
+  const float mb = -m_run * LOG2E;
 
-  // O^T[d][query] += V^T[d][keys] . P^T[keys][query]; a step whose 32 keys are all past L adds
-  // nothing and is skipped.
-  constexpr int NKS = (NKB + 1) / 2;
+  // P = 2^(S log2e - m_run log2e) in f16; O^T[d][query] += V^T[d][keys] . P^T[keys][query] over
+  // the 16-key steps of the valid halves, the P^T operand of step c being registers
+  // 8 (c % 2) .. +7 of half c / 2; l += the f16 P, two at a time (v_dot2 with (1, 1))
+  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
-  for (int ks = 0; ks < NKS; ks++)
+  for (int c = 0; c < 2 * NS; c++) {
+    h8 pb;
 #pragma unroll
-    for (int db = 0; db < 4; db++)
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v_operand(Vb, ks, db, lane), pb[ks], o[db], 0, 0, 0);
+    for (int j = 0; j < 8; j++)
+      pb[j] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + j], LOG2E, mb));
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) l_run = __builtin_amdgcn_fdot2(h2{pb[j], pb[j + 1]}, ones, l_run, false);
+#pragma unroll
+    for (int db = 0; db < 2; db++) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[c][db], pb, o[db], 0, 0, 0);
+  }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attn_relbias_kernel(AttnArgs p) {
-  // double-buffered tiles as separate objects, so that the loads into one buffer are not
-  // waited on by the reads of the other
-  __shared__ __attribute__((aligned(16))) _Float16 Ks0[KT * DK], Ks1[KT * DK];
-  __shared__ __attribute__((aligned(16))) _Float16 Vs0[KT * DK], Vs1[KT * DK];
-  __shared__ __attribute__((aligned(16))) float Bs0[2 * KT], Bs1[2 * KT];
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) void attn_relbias_kernel(AttnArgs p) {
+  __shared__ Slot S0, S1, S2;  // the ring; tile t lives in slot t % 3
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int4 wk = p.work[blockIdx.x];
-  const int s0 = wk.x, L = wk.y, q0 = wk.z, h = wk.w;
+  const int s0 = wk.x, L = wk.y, q0 = wk.z, hd = wk.w;
   if (L == 0) return;  // an empty slot of the work list (the whole workgroup)
-  const int lr = lane & 15, lg = lane >> 4;
+  const int l32 = lane & 31, h = lane >> 5;
 
   const size_t head_stride = (size_t)p.tpad * DK;
-  const _Float16* Q = p.qkv + ((size_t)0 * p.heads + h) * head_stride + (size_t)s0 * DK;
-  const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + h) * head_stride + (size_t)s0 * DK;
-  const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + h) * head_stride + (size_t)s0 * DK;
-  // bias of distance d = j - i at lut[d], |d| <= lutw (lutw >= padded sequence length + 1)
-  const float* lut = p.lut + (size_t)h * (2 * p.lutw + 1) + p.lutw;
-  // the bias of every distance <= -sat and of every distance >= sat
-  const float bias_far[2] = {lut[-p.lutw], lut[p.lutw]};
-  // A middle tile (not the first or the last, which always read the staged bias) whose
-  // distances to every query of the workgroup are that far needs no bias values.
-  auto stage_bias = [&](int k0) {
-    return k0 == 0 || k0 + KT >= L || !(k0 - q0 - (QT - 1) >= p.sat || k0 + KT - 1 - q0 <= -p.sat);
-  };
+  const _Float16* Q = p.qkv + ((size_t)0 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  // bias of distance d = j - i at lut[d], |d| <= lutw (lutw >= padded sequence length + QT)
+  const float* lut = p.lut + (size_t)hd * (2 * p.lutw + 1) + p.lutw;
 
-  // This lane's query (relative to the sequence start).  Queries past L compute on
-  // in-bounds padding rows and are never stored.
-  const int qi = q0 + wave * 16 + lr;
-  h8 qf[2];
-  qf[0] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + lg * 8);
-  qf[1] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 32 + lg * 8);
+  // This lane's query (relative to the sequence start).  Queries past L compute on in-bounds
+  // padding rows and are never stored.
+  const int qi = q0 + wave * QW + l32;
+  h8 qf[4];
 
-  // tile loads straight into LDS: K and V rows k0.. (clamped to the sequence), and the 128 bias
-  // values of distances k0 - q0 - 63 .. k0 - q0 + 64 by waves 0 and 1
-  auto load_tile = [&](int k0, _Float16* Kd, _Float16* Vd, float* Bd) {
+  // A tile's loads, the same five per wave for every tile: K and V rows k0.. (clamped to the
+  // sequence) and 64 of the bias values of distances k0 - q0 - (QT - 1) .. (QT + KT - 1 of the
+  // 256 staged are read).
+  auto load_tile = [&](int k0, _Float16* Kd, _Float16* Vd, float* Bd) __attribute__((always_inline)) {
     dma_tile(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
     dma_tile(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
-    if (wave < 2 && stage_bias(k0))
-      __builtin_amdgcn_global_load_lds(lut + (k0 - q0 - (QT - 1) + 64 * wave + lane), Bd + 64 * wave, 4, 0, 0);
+    lds_load4(lut + (k0 - q0 - (QT - 1) + 64 * wave + lane), lds_offset(Bd + 64 * wave));
   };
+  static_assert(LOADS == 5, "the wait below counts five loads per tile");
 
   float m_run = -INFINITY, l_run = 0.f;
-  f4 o[4];
+  f16v o[2];
 #pragma unroll
-  for (int i = 0; i < 4; i++) o[i] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[db][r] = 0.f;
 
   const int ntile = (L + KT - 1) / KT;
-  // Bs index of this lane's (key 4lg + i of key block 0, query qi): (j - qi) - (k0 - q0 - 63)
-  const int bofs = (QT - 1) - wave * 16 - lr + 4 * lg;
-  // Waves whose 16 queries all lie past L (in a sequence's last query tile) only help load
-  // the tiles.  The test is wave-uniform.
-  const bool active = q0 + wave * 16 < L;
-  // The first tile sets the reference max; the middle tiles are full; the last one holds keys
-  // past L unless L is a multiple of 64 (rem = 0).  A single tile is both first and last.
-  const int rem = L & (KT - 1);
-  // one tile: issue the next tile's loads into the other buffer, compute this one, wait for
-  // this wave's loads and meet the other waves
-  auto step = [&](int t, const _Float16* Kc, const _Float16* Vc, const float* Bc, _Float16* Kn, _Float16* Vn,
-                  float* Bn, auto&& compute) {
-    if (t + 1 < ntile) load_tile((t + 1) * KT, Kn, Vn, Bn);
-    if (active) compute(Kc, Vc, Bc, t * KT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  // Bs index of this lane's (key 4h + r of the tile, query qi): (j - qi) - (k0 - q0 - (QT - 1))
+  const int bofs = (QT - 1) - wave * QW - l32 + 4 * h;
+  const LaneOfs lofs = lane_offsets(lane);
+  // Tile t lives in slot t % 3.  Step t waits for this wave's loads of tile t (those of t + 1
+  // may still be in flight), meets the other waves (every wave's part of tile t has landed, and
+  // every wave is done with tile t - 1), issues tile t + 2 into the slot tile t - 1 used, then
+  // computes tile t.  Every tile but the last is full; the last one holds keys past L unless L
+  // is a multiple of 64, and its second half holds none below L when L - k0 <= 32.
+  // act: whether this wave computes (below); tail: whether t may be the last tile.
+  auto step = [&](auto act, auto tail, int t, const Slot& cur, Slot& next) __attribute__((always_inline)) {
+    const bool last = decltype(tail)::value && t + 1 == ntile;
+    // lgkmcnt(0): this wave's LDS reads of tile t - 1 have completed before any wave may refill
+    // that slot (the compiler may have sunk their products past this point)
+    if (!last) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (t + 2 < ntile) load_tile((t + 2) * KT, next.k, next.v, next.b);
+    if (!decltype(act)::value) return;
+    const int k0 = t * KT;
+    if (!last) attn_tile<true, false>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
+    else if (L - k0 > 32) attn_tile<true, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
+    else attn_tile<false, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
   };
-  auto middle = [&](const _Float16* Kc, const _Float16* Vc, const float* Bc, int k0) {
-    const int qa = q0 + wave * 16;  // this wave's distances j - i span [k0 - qa - 15, k0 + 63 - qa]
-    if (k0 - qa - 15 >= p.sat || k0 + KT - 1 - qa <= -p.sat)
-      attn_tile<4, false, false, true>(Kc, Vc, Bc, bofs, k0 > qa ? bias_far[1] : bias_far[0], qf, k0, L, m_run,
-                                       l_run, o);
-    else
-      attn_tile<4, false, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o);
-  };
-  auto last = [&](const _Float16* Kc, const _Float16* Vc, const float* Bc, int k0) {
-    if (rem == 0) {
-      attn_tile<4, false, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o);
-    } else {
-      switch ((rem + 15) >> 4) {
-        case 1: attn_tile<1, true, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        case 2: attn_tile<2, true, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        case 3: attn_tile<3, true, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        default: attn_tile<4, true, false, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-      }
+  // The Q loads complete before tile 0, which is peeled off the loop, so that the loop body (whose
+  // steps are never the last tile) carries a single tile variant and no wait on them.
+  auto run = [&](auto act) __attribute__((always_inline)) {
+    constexpr std::false_type body{};
+    constexpr std::true_type tail{};
+    load_tile(0, S0.k, S0.v, S0.b);
+    if (ntile > 1) load_tile(KT, S1.k, S1.v, S1.b);
+    if (decltype(act)::value) {
+#pragma unroll
+      for (int ds = 0; ds < 4; ds++) qf[ds] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 16 * ds + 8 * h);
+      // The empty asm reads and redefines qf, so the compiler completes the Q loads here (its
+      // wait also covers the first two tiles, issued just before) and no step waits on them.
+      asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]));
     }
-  };
-
-  load_tile(0, Ks0, Vs0, Bs0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  step(0, Ks0, Vs0, Bs0, Ks1, Vs1, Bs1, [&](const _Float16* Kc, const _Float16* Vc, const float* Bc, int k0) {
-    if (ntile > 1 || rem == 0) {
-      attn_tile<4, false, true, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o);
-    } else {
-      switch ((rem + 15) >> 4) {
-        case 1: attn_tile<1, true, true, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        case 2: attn_tile<2, true, true, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        case 3: attn_tile<3, true, true, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-        default: attn_tile<4, true, true, false>(Kc, Vc, Bc, bofs, 0.f, qf, k0, L, m_run, l_run, o); break;
-      }
+    step(act, tail, 0, S0, S2);
+    int t = 1;
+    for (; t + 3 < ntile; t += 3) {
+      step(act, body, t, S1, S0);
+      step(act, body, t + 1, S2, S1);
+      step(act, body, t + 2, S0, S2);
     }
-  });
-  // middle tiles in pairs (odd tiles in buffer 1, even ones in buffer 0), then the last tile
-  int t = 1;
-  for (; t + 2 < ntile; t += 2) {
-    step(t, Ks1, Vs1, Bs1, Ks0, Vs0, Bs0, middle);
-    step(t + 1, Ks0, Vs0, Bs0, Ks1, Vs1, Bs1, middle);
-  }
-  if (t + 1 < ntile) {
-    step(t, Ks1, Vs1, Bs1, Ks0, Vs0, Bs0, middle);
-    t++;
-  }
-  if (t < ntile) {
-    if (t & 1) step(t, Ks1, Vs1, Bs1, Ks0, Vs0, Bs0, last);
-    else step(t, Ks0, Vs0, Bs0, Ks1, Vs1, Bs1, last);
-  }
-  l_run = sum_xor32(sum_xor16(l_run));
+    if (t < ntile) step(act, tail, t, S1, S0);
+    if (t + 1 < ntile) step(act, tail, t + 1, S2, S1);
+    if (t + 2 < ntile) step(act, tail, t + 2, S0, S2);
+  };
+  // Waves whose 32 queries all lie past L (in a sequence's last query tile) only help load the
+  // tiles, through the same waits and barriers.  The test is wave-uniform.
+  const bool active = q0 + wave * QW < L;
+  if (active) run(std::true_type{});
+  else run(std::false_type{});
+  l_run = sum_xor32(l_run);
 
-  if (qi < L) {  // written in operand order for the O GEMM
+  if (active && qi < L) {  // written in operand order for the O GEMM
     const float inv = 1.0f / l_run;
     const int inner = p.heads * DK;
 #pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const h4 v = {(_Float16)(o[db][0] * inv), (_Float16)(o[db][1] * inv), (_Float16)(o[db][2] * inv),
-                    (_Float16)(o[db][3] * inv)};
-      *reinterpret_cast<h4*>(p.out + tiled_index(s0 + qi, h * DK + db * 16 + lg * 4, inner)) = v;
-    }
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+      for (int a = 0; a < 4; a++) {
+        const h4 v = {(_Float16)(o[db][4 * a] * inv), (_Float16)(o[db][4 * a + 1] * inv),
+                      (_Float16)(o[db][4 * a + 2] * inv), (_Float16)(o[db][4 * a + 3] * inv)};
+        *reinterpret_cast<h4*>(p.out + tiled_index(s0 + qi, hd * DK + 32 * db + 8 * a + 4 * h, inner)) = v;
+      }
   }
 }
 
@@ -302,7 +329,7 @@ hipError_t launch_attention(const AttnArgs& a, int n_work, int dkv, hipStream_t 
   if (n_work <= 0) return hipSuccess;
   // one workgroup per work item; item b runs on XCD b % 8, and the list keeps all query tiles of
   // a (sequence, head) on one XCD so that its keys and values stay in that XCD's L2
-  T5K_LAUNCH(attn_relbias_kernel, dim3((unsigned)n_work), dim3(256), 0, s, a);
+  T5K_LAUNCH(attn_relbias_kernel, dim3((unsigned)n_work), dim3(64 * NWV), 0, s, a);
   return hipGetLastError();
 }
 }  // namespace t5k
