@@ -48,14 +48,18 @@ struct __attribute__((aligned(16))) Slot {
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 // LDS tiles are 64 keys x 64 dims of f16, 128 B rows of eight 16-byte chunks; chunk c of row r
-// sits at position c ^ rot(r), rot(r) = r's low three bits with bits 1 and 2 swapped.  The
-// rotation is a bijection on each 8 rows, so the K operand reads (8 rows x one chunk per 8
-// lanes) are conflict-free, and it sends rows r and r + 2 to opposite 64-byte halves of a row, so
-// a transposed V read (per 32 lanes 4 consecutive rows x 4 chunks, 256 B over the 64 banks,
-// where rows r and r + 2 share bank offsets) is conflict-free as well; the plain r % 8 rotation
-// gives 2-way conflicts there.
-__device__ __forceinline__ int rot(int row) { return (row & 1) | ((row & 2) << 1) | ((row & 4) >> 1); }
-__device__ __forceinline__ int swz(int row, int col) { return row * DK + ((((col >> 3) ^ rot(row)) & 7) << 3) + (col & 7); }
+// sits at position c ^ rot(r).  Both rotations are bijections on each 8 consecutive rows.  The V
+// tile uses rot_v(r) = r's low three bits with bits 1 and 2 swapped, the K tile rot_k(r) =
+// (r ^ (r >> 2)) % 8: with them the transposed V reads and the K operand reads are free of bank
+// conflicts (SQ_LDS_BANK_CONFLICT reads 0 for each pattern alone on gfx950), where the plain
+// r % 8 rotation costs 2-way conflicts on both.  rot_k(r + 32) = rot_k(r), and both depend on
+// no higher row bits than that, so key offsets of 8, 16 and 32 rows fold into immediates.
+__device__ __forceinline__ int rot_v(int row) { return (row & 1) | ((row & 2) << 1) | ((row & 4) >> 1); }
+__device__ __forceinline__ int rot_k(int row) { return (row ^ (row >> 2)) & 7; }
+template <bool KT_>
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * DK + ((((col >> 3) ^ (KT_ ? rot_k(row) : rot_v(row))) & 7) << 3) + (col & 7);
+}
 
 // Global -> LDS loads (global_load_lds), written as inline asm so that the compiler does not
 // track them: its tracking waits for every outstanding one before a read of one of the ring
@@ -75,14 +79,16 @@ __device__ __forceinline__ void lds_load4(const void* src, uint32_t m0) {
 }
 
 // Global -> LDS copy of one 64-row tile by this wave's 16 rows: LDS slot l of an instruction
-// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ rot(row), so
-// each group of 8 lanes still reads one 128-byte row.  Rows at or past `nrows` repeat the last
-// row of the sequence: finite values, which the masked scores (P = 0) then ignore.
+// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ rot(row) (rot_k
+// for a K tile), so each group of 8 lanes still reads one 128-byte row.  Rows at or past
+// `nrows` repeat the last row of the sequence: finite values, which the masked scores (P = 0)
+// then ignore.
+template <bool KT_>
 __device__ __forceinline__ void dma_tile(const _Float16* src, int nrows, _Float16* dst, int wave, int lane) {
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int row = 16 * wave + 8 * j + (lane >> 3);
-    const int chunk = (lane ^ rot(row)) & 7;
+    const int chunk = (lane ^ (KT_ ? rot_k(row) : rot_v(row))) & 7;
     const int srow = row < nrows ? row : nrows - 1;
     lds_load16(src + (size_t)srow * DK + chunk * 8, lds_offset(dst + (16 * wave + 8 * j) * DK));
   }
@@ -100,9 +106,9 @@ __device__ __forceinline__ LaneOfs lane_offsets(int lane) {
   const int l32 = lane & 31, h = lane >> 5, i = lane & 15, g = lane >> 4;
   LaneOfs o;
 #pragma unroll
-  for (int ds = 0; ds < 4; ds++) o.k[ds] = swz(l32, 16 * ds + 8 * h);
+  for (int ds = 0; ds < 4; ds++) o.k[ds] = swz<true>(l32, 16 * ds + 8 * h);
 #pragma unroll
-  for (int db = 0; db < 2; db++) o.v[db] = swz(4 * h + (i >> 2), 32 * db + 16 * (g & 1) + 4 * (i & 3));
+  for (int db = 0; db < 2; db++) o.v[db] = swz<false>(4 * h + (i >> 2), 32 * db + 16 * (g & 1) + 4 * (i & 3));
   return o;
 }
 
@@ -239,8 +245,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
   // sequence) and 64 of the bias values of distances k0 - q0 - (QT - 1) .. (QT + KT - 1 of the
   // 256 staged are read).
   auto load_tile = [&](int k0, _Float16* Kd, _Float16* Vd, float* Bd) __attribute__((always_inline)) {
-    dma_tile(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
-    dma_tile(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
+    dma_tile<true>(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
+    dma_tile<false>(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
     lds_load4(lut + (k0 - q0 - (QT - 1) + 64 * wave + lane), lds_offset(Bd + 64 * wave));
   };
   static_assert(LOADS == 5, "the wait below counts five loads per tile");
