@@ -144,7 +144,7 @@ __device__ __forceinline__ h8 v_operand(const _Float16* Vb, int c, int vo) {
 // a query only at the end.
 template <bool FULL, bool MASK>
 __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* Vb, const float* Bsb, int bofs,
-                                          LaneOfs lo, const h8 (&qf)[4], int k0, int L, float& m_run,
+                                          LaneOfs lo, const h8 (&qf)[4], bool qv, int k0, int L, float& m_run,
                                           float& l_run, f16v (&o)[2]) {
   constexpr int NS = FULL ? 2 : 1;  // 32-key halves with keys < L
   const int h = (threadIdx.x >> 5) & 1;
@@ -191,7 +191,10 @@ __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* V
 #pragma unroll
     for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
   mx = max_xor32(mx);  // finite: key k0 < L is valid
-  if (__any(!((mx - m_run) * LOG2E <= 14.f))) {  // !(x <= 14) also catches NaN
+  // Only lanes of queries below L take part (qv), so that whatever the rows past L hold cannot
+  // change when the valid queries rescale: the result stays independent of the batch around
+  // the sequence.  !(x <= 14) also catches NaN.
+  if (__any(qv && !((mx - m_run) * LOG2E <= 14.f))) {
     // the rescale of O sits in a branch of its own, so the accumulators keep their registers
     const float m_new = fmaxf(m_run, mx);
     // 1 where the max did not move, 0 on the first tile (O and l are still 0 there)
@@ -277,9 +280,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
     if (t + 2 < ntile) load_tile((t + 2) * KT, next.k, next.v, next.b);
     if (!decltype(act)::value) return;
     const int k0 = t * KT;
-    if (!last) attn_tile<true, false>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
-    else if (L - k0 > 32) attn_tile<true, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
-    else attn_tile<false, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, k0, L, m_run, l_run, o);
+    if (!last) attn_tile<true, false>(cur.k, cur.v, cur.b, bofs, lofs, qf, qi < L, k0, L, m_run, l_run, o);
+    else if (L - k0 > 32) attn_tile<true, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, qi < L, k0, L, m_run, l_run, o);
+    else attn_tile<false, true>(cur.k, cur.v, cur.b, bofs, lofs, qf, qi < L, k0, L, m_run, l_run, o);
   };
   // The Q loads complete before tile 0, which is peeled off the loop, so that the loop body (whose
   // steps are never the last tile) carries a single tile variant and no wait on them.
