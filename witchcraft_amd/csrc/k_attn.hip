@@ -48,17 +48,22 @@ struct __attribute__((aligned(16))) Slot {
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 // LDS tiles are 64 keys x 64 dims of f16, 128 B rows of eight 16-byte chunks; chunk c of row r
-// sits at position c ^ rot(r).  Both rotations are bijections on each 8 consecutive rows.  The V
-// tile uses rot_v(r) = r's low three bits with bits 1 and 2 swapped, the K tile rot_k(r) =
-// (r ^ (r >> 2)) % 8: with them the transposed V reads and the K operand reads are free of bank
-// conflicts (SQ_LDS_BANK_CONFLICT reads 0 for each pattern alone on gfx950), where the plain
-// r % 8 rotation costs 2-way conflicts on both.  rot_k(r + 32) = rot_k(r), and both depend on
-// no higher row bits than that, so key offsets of 8, 16 and 32 rows fold into immediates.
-__device__ __forceinline__ int rot_v(int row) { return (row & 1) | ((row & 2) << 1) | ((row & 4) >> 1); }
-__device__ __forceinline__ int rot_k(int row) { return (row ^ (row >> 2)) & 7; }
-template <bool KT_>
+// sits at position c ^ rot(r).  Each rotation is a bijection on each 8 consecutive rows.  The V
+// tile uses ROT_V(r) = r's low three bits with bits 1 and 2 swapped, the K tile ROT_K(r) =
+// (r ^ (r >> 2)) % 8: with them the transposed V reads and the K operand reads of the 32-query
+// waves are free of bank conflicts (SQ_LDS_BANK_CONFLICT reads 0 for each pattern alone on
+// gfx950), where the plain ROT_8(r) = r % 8 costs 2-way conflicts on both.  The 16-query waves
+// of a short sequence read 16 rows per K operand and 4 rows x 2 chunks per 16 lanes of V, which
+// ROT_8 serves without conflicts.  ROT_K(r + 32) = ROT_K(r), and none depends on higher row
+// bits than that, so key offsets of 8, 16 and 32 rows fold into immediates.
+enum { ROT_V = 0, ROT_K = 1, ROT_8 = 2 };
+template <int R>
+__device__ __forceinline__ int rot(int row) {
+  return R == ROT_V ? ((row & 1) | ((row & 2) << 1) | ((row & 4) >> 1)) : R == ROT_K ? ((row ^ (row >> 2)) & 7) : (row & 7);
+}
+template <int R>
 __device__ __forceinline__ int swz(int row, int col) {
-  return row * DK + ((((col >> 3) ^ (KT_ ? rot_k(row) : rot_v(row))) & 7) << 3) + (col & 7);
+  return row * DK + ((((col >> 3) ^ rot<R>(row)) & 7) << 3) + (col & 7);
 }
 
 // Global -> LDS loads (global_load_lds), written as inline asm so that the compiler does not
@@ -79,16 +84,16 @@ __device__ __forceinline__ void lds_load4(const void* src, uint32_t m0) {
 }
 
 // Global -> LDS copy of one 64-row tile by this wave's 16 rows: LDS slot l of an instruction
-// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ rot(row) (rot_k
-// for a K tile), so each group of 8 lanes still reads one 128-byte row.  Rows at or past
+// (16 B, consecutive by lane) holds row 16 wave + 8 j + l / 8, chunk (l % 8) ^ rot<R>(row), so
+// each group of 8 lanes still reads one 128-byte row.  Rows at or past
 // `nrows` repeat the last row of the sequence: finite values, which the masked scores (P = 0)
 // then ignore.
-template <bool KT_>
+template <int R>
 __device__ __forceinline__ void dma_tile(const _Float16* src, int nrows, _Float16* dst, int wave, int lane) {
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int row = 16 * wave + 8 * j + (lane >> 3);
-    const int chunk = (lane ^ (KT_ ? rot_k(row) : rot_v(row))) & 7;
+    const int chunk = (lane ^ rot<R>(row)) & 7;
     const int srow = row < nrows ? row : nrows - 1;
     lds_load16(src + (size_t)srow * DK + chunk * 8, lds_offset(dst + (16 * wave + 8 * j) * DK));
   }
@@ -106,9 +111,9 @@ __device__ __forceinline__ LaneOfs lane_offsets(int lane) {
   const int l32 = lane & 31, h = lane >> 5, i = lane & 15, g = lane >> 4;
   LaneOfs o;
 #pragma unroll
-  for (int ds = 0; ds < 4; ds++) o.k[ds] = swz<true>(l32, 16 * ds + 8 * h);
+  for (int ds = 0; ds < 4; ds++) o.k[ds] = swz<ROT_K>(l32, 16 * ds + 8 * h);
 #pragma unroll
-  for (int db = 0; db < 2; db++) o.v[db] = swz<false>(4 * h + (i >> 2), 32 * db + 16 * (g & 1) + 4 * (i & 3));
+  for (int db = 0; db < 2; db++) o.v[db] = swz<ROT_V>(4 * h + (i >> 2), 32 * db + 16 * (g & 1) + 4 * (i & 3));
   return o;
 }
 
@@ -223,6 +228,118 @@ __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* V
   }
 }
 
+// A sequence of at most 64 tokens: one key tile and at most 64 queries, taken by the four waves
+// as 16 queries each on v_mfma_f32_16x16x32_f16 -- half the chain of dependent work per wave of
+// the 32-query path, which is what bounds such short launches -- and with no running max: the
+// tile's own max is the reference.  Whether a sequence takes this path depends on its length
+// only, so its result does not depend on the batch around it.
+//
+// Layouts of the 16x16x32 product: A lane l = row l % 16, K 8 (l / 16) .. +7; B lane l = column
+// l % 16, the same K; D lane l register i = row 4 (l / 16) + i, column l % 16.  S^T = K . Q^T in
+// key blocks of 16, so lane (lr, lg) = (l % 16, l / 16) holds query lr against keys
+// 16 kb + 4 lg + i; the P^T operand of key step ks (32 keys) is then registers 0..3 of blocks
+// 2 ks and 2 ks + 1, keys {32 ks + 4 lg + i, 32 ks + 16 + 4 lg + i}, and the V^T operand is read
+// in that key order.
+template <int NKB>
+__device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* Vs, const float* Bs, const h8 (&qf)[2],
+                                           int L, int s0, int hd, int qi, const AttnArgs& p) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4, wave = threadIdx.x >> 6;
+  constexpr int NKS = (NKB + 1) / 2;  // 32-key P.V steps holding keys < L
+  // bias of (key j, query i) staged at j - i + 63
+  const int bofs = 63 - 16 * wave - lr + 4 * lg;
+  f4 s[2 * NKS];
+#pragma unroll
+  for (int kb = 0; kb < 2 * NKS; kb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) s[kb][i] = kb < NKB ? Bs[bofs + 16 * kb + i] : 0.f;
+#pragma unroll
+  for (int ds = 0; ds < 2; ds++)
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+      const h8 a = *reinterpret_cast<const h8*>(&Ks[swz<ROT_8>(16 * kb + lr, 32 * ds + 8 * lg)]);
+      s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
+    }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 2 * NKS; kb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (kb >= NKB || 16 * kb + 4 * lg + i >= L) s[kb][i] = -INFINITY;  // keys past L
+      mx = fmaxf(mx, s[kb][i]);
+    }
+  mx = max_xor32(max_xor16(mx));  // finite: key 0 < L
+  const float mb = -mx * LOG2E;
+  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
+  float l = 0.f;
+  h8 pb[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ks++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      pb[ks][i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * ks][i], LOG2E, mb));
+      pb[ks][4 + i] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * ks + 1][i], LOG2E, mb));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) l = __builtin_amdgcn_fdot2(h2{pb[ks][j], pb[ks][j + 1]}, ones, l, false);
+  }
+  l = sum_xor32(sum_xor16(l));
+  // O^T[d][query] = V^T[d][keys] . P^T[keys][query]: lane (n, g) = (l % 16, l / 16) of 16-lane group g
+  // reads rows 32 ks + 4 g + i / 4 (+ 16), dims 16 db + 4 (i % 4); the transposing read returns
+  // V[32 ks + 4 g + r][16 db + n] (and 16 rows on), the keys of its P^T slots.
+  typedef __attribute__((address_space(3))) s4v lds_s4;
+  f4 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; db++) {
+    o[db] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const int row = 32 * ks + 4 * lg + (lr >> 2), col = 16 * db + 4 * (lr & 3);
+      const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vs + swz<ROT_8>(row, col)));
+      const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vs + swz<ROT_8>(row + 16, col)));
+      h8 v;
+      __builtin_memcpy(&v, &lo, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&v) + 8, &hi, 8);
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v, pb[ks], o[db], 0, 0, 0);
+    }
+  }
+  if (qi < L) {  // written in operand order for the O GEMM
+    const float inv = 1.0f / l;
+    const int inner = p.heads * DK;
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+      *reinterpret_cast<h4*>(p.out + tiled_index(s0 + qi, hd * DK + 16 * db + 4 * lg, inner)) =
+          h4{(_Float16)(o[db][0] * inv), (_Float16)(o[db][1] * inv), (_Float16)(o[db][2] * inv),
+             (_Float16)(o[db][3] * inv)};
+  }
+}
+
+__device__ __forceinline__ void short_sequence(const AttnArgs& p, Slot& sl, int s0, int L, int hd, int wave, int lane) {
+  const size_t head_stride = (size_t)p.tpad * DK;
+  const _Float16* Q = p.qkv + ((size_t)0 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + hd) * head_stride + (size_t)s0 * DK;
+  const float* lut = p.lut + (size_t)hd * (2 * p.lutw + 1) + p.lutw;
+  // the tile (rows past L repeat the last row) and the bias of distances -63 .. 64
+  dma_tile<ROT_8>(Kg, L, sl.k, wave, lane);
+  dma_tile<ROT_8>(Vg, L, sl.v, wave, lane);
+  if (wave < 2) lds_load4(lut + (64 * wave - 63 + lane), lds_offset(sl.b + 64 * wave));
+  const int lr = lane & 15, lg = lane >> 4, qi = 16 * wave + lr;
+  const bool active = 16 * wave < L;  // wave-uniform
+  h8 qf[2];
+  if (active) {
+    qf[0] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 8 * lg);
+    qf[1] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 32 + 8 * lg);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (!active) return;
+  switch ((L + 15) >> 4) {
+    case 1: short_tile<1>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
+    case 2: short_tile<2>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
+    case 3: short_tile<3>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
+    default: short_tile<4>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
+  }
+}
+
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) void attn_relbias_kernel(AttnArgs p) {
   __shared__ Slot S0, S1, S2;  // the ring; tile t lives in slot t % 3
 
@@ -230,6 +347,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
   const int4 wk = p.work[blockIdx.x];
   const int s0 = wk.x, L = wk.y, q0 = wk.z, hd = wk.w;
   if (L == 0) return;  // an empty slot of the work list (the whole workgroup)
+  if (L <= KT) {        // one key tile, one query tile (uniform across the workgroup)
+    short_sequence(p, S0, s0, L, hd, wave, lane);
+    return;
+  }
   const int l32 = lane & 31, h = lane >> 5;
 
   const size_t head_stride = (size_t)p.tpad * DK;
@@ -248,8 +369,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
   // sequence) and 64 of the bias values of distances k0 - q0 - (QT - 1) .. (QT + KT - 1 of the
   // 256 staged are read).
   auto load_tile = [&](int k0, _Float16* Kd, _Float16* Vd, float* Bd) __attribute__((always_inline)) {
-    dma_tile<true>(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
-    dma_tile<false>(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
+    dma_tile<ROT_K>(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
+    dma_tile<ROT_V>(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
     lds_load4(lut + (k0 - q0 - (QT - 1) + 64 * wave + lane), lds_offset(Bd + 64 * wave));
   };
   static_assert(LOADS == 5, "the wait below counts five loads per tile");
