@@ -755,11 +755,11 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   return T5H_OK;
 }
 
-// Attention work plan.  One workgroup per (sequence, head, 64 queries); workgroup b runs on
+// Attention work plan.  One workgroup per (sequence, head, ATTN_QT queries); workgroup b runs on
 // XCD b % 8 (workgroups are dealt round-robin), so the list is laid out as 8 interleaved
 // per-XCD lists.  All query tiles of one (sequence, head) go to one XCD, one after another, so
 // that XCD's L2 holds the group's keys and values while its query tiles stream them (2048
-// tokens: 512 KB per group, read by 32 workgroups).  Groups are taken longest sequence first
+// tokens: 512 KB per group, read by 16 workgroups).  Groups are taken longest sequence first
 // and each goes to the XCD with the least work (query tiles x key tiles) among those whose
 // list stays within ceil(items / 8) + the longest group, which bounds the padding: the lists
 // are padded to the longest one with empty items (length 0), which exit at once.
