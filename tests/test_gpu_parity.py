@@ -114,8 +114,21 @@ def test_small_model_ragged_batch(small):
     _check_batch(gpu, ora, ids, cu)
 
 
+def test_small_model_ragged_batch_tile_boundaries(small):
+    """Lengths at the attention's key-tile (64), half-tile (32) and 128-query tile edges: one-tile
+    sequences, last tiles with one or two valid 32-key halves, and second query tiles of 1 to
+    128 queries."""
+    cfg, _, gpu, ora = small
+    lens = [66, 96, 97, 127, 128, 129, 160, 161, 191, 192, 193, 255, 256, 32, 33]
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = np.random.default_rng(4).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    _check_batch(gpu, ora, ids, cu)
+
+
 def test_small_model_ragged_batch_past_four_key_tiles(small):
-    """5 to 8 key tiles of 64 per sequence: the attention's 4-slot load ring wraps part-way."""
+    """5 to 8 key tiles of 64 per sequence: the attention's three-slot load ring wraps more than
+    once, through both the loop body and the steps after it."""
     cfg, _, gpu, ora = small
     lens = [257, 300, 383, 420, 449, 512, 33]
     cu = np.zeros(len(lens) + 1, np.int32)
