@@ -13,7 +13,8 @@
 // Keys are streamed in tiles of 64 through a three-deep LDS ring with an online softmax.  The
 // tiles travel global -> LDS without registers (global_load_lds_dwordx4): K and V rows as they
 // lie in memory, 128 B per key, and the bias values a tile needs (by j - i).  A tile's loads
-// are issued two tiles ahead; one barrier per tile.
+// are issued two tiles ahead; one barrier per tile.  A sequence of at most 64 tokens takes a
+// one-tile path with 16-query waves instead (short_sequence).
 //
 // The score block is computed transposed, S^T = K . Q^T (32 keys x 32 queries per MFMA), so
 // that the accumulator layout (lane = query column; lane half h holds keys 8a + 4h + b) is, four
