@@ -126,6 +126,27 @@ def test_small_model_ragged_batch_tile_boundaries(small):
     _check_batch(gpu, ora, ids, cu)
 
 
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_small_model_random_ragged_batches(small, seed):
+    """Random compositions: 1 to 600 tokens per sequence, shuffled, with the sequences also
+    encoded in a second order (each sequence's rows must not depend on its neighbours)."""
+    cfg, _, gpu, ora = small
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, 601, size=8)
+    cu = np.zeros(len(lens) + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    _check_batch(gpu, ora, ids, cu)
+    out, _ = gpu.encode_packed(ids, cu)
+    perm = rng.permutation(len(lens))
+    ids2 = np.concatenate([ids[cu[b]:cu[b + 1]] for b in perm])
+    cu2 = np.zeros_like(cu)
+    cu2[1:] = np.cumsum(lens[perm])
+    out2, _ = gpu.encode_packed(ids2, cu2)
+    for j, b in enumerate(perm):
+        assert np.array_equal(out2[cu2[j]:cu2[j + 1]].view(np.uint32), out[cu[b]:cu[b + 1]].view(np.uint32)), (b, lens[b])
+
+
 def test_small_model_ragged_batch_past_four_key_tiles(small):
     """5 to 8 key tiles of 64 per sequence: the attention's three-slot load ring wraps more than
     once, through both the loop body and the steps after it."""
