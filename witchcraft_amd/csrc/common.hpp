@@ -131,7 +131,6 @@ struct AttnArgs {
   const int4* work;     // (sequence start, length, first query, head) per workgroup; length 0: empty
   const float* lut;     // [H][2*lutw+1] relative bias by (j - i), centred at lutw
   int heads, tpad, lutw;
-  int sat;  // lut[d] = lut[lutw] for d >= sat and lut[-d] = lut[-lutw] (the buckets saturate)
 };
 
 // Device-side helpers ---------------------------------------------------------

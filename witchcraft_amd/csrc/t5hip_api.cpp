@@ -229,7 +229,7 @@ struct t5h_model {
   const void* emb = nullptr;
   int emb_fmt = EMB_F32;
   const float* rel_lut = nullptr;  // [H][2*lutw+1], bias of distance j - i at lutw + j - i
-  int lutw = 0, lut_sat = 0;  // lut_sat: |j - i| from which the bias is the LUT's end value
+  int lutw = 0;
   std::vector<int> order;  // host scratch: sequence order of the attention work list
   std::vector<int32_t> last_cu;  // cu_seqlens of the batch whose cu / work list are on the device
   int last_B = -1, last_nwork = 0;
@@ -977,7 +977,6 @@ int run_block(t5h_model* m, int l, int T, int nwork, bool operand_ready = false,
     a.heads = c.num_heads;
     a.tpad = m->w.tpad;
     a.lutw = m->lutw;
-    a.sat = m->lut_sat;
     Timed t(m, K_ATTN, m->attn_flops, 0);
     HIP_OK(t5k::launch_attention(a, nwork, c.d_kv, m->stream));
     if (m->prof) {
@@ -1567,9 +1566,9 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
   if (rb->type != t5h::GGML_F32 || rb->shape.size() != 2 ||
       (int)rb->rows() != cfg->relative_attention_num_buckets || (int)rb->cols() != H)
     return fail(T5H_ERR_FORMAT, "tensor " + rb_name + ": expected F32 [num_buckets, num_heads]");
-  // The attention kernel stages the bias of distances k0 - q0 - (ATTN_QT - 1) .. k0 - q0 + 64
-  // (64-key tiles, ATTN_QT-query workgroups), so the LUT covers |j - i| <= roundup(max_seq_len,
-  // 64) + ATTN_QT.
+  // The attention kernel stages the bias of distances k0 - q0 - (ATTN_QT - 1) .. k0 - q0 + 128
+  // for a 64-key tile and an ATTN_QT-query workgroup (256 values, 4 waves x 64), so the LUT
+  // covers |j - i| <= roundup(max_seq_len, 64) + ATTN_QT.
   const int lutw = (cfg->max_seq_len + 63) / 64 * 64 + ATTN_QT, span = 2 * lutw + 1;
   const size_t lut_off = ha.add(nullptr, (size_t)H * span * 4);
   {
@@ -1581,15 +1580,6 @@ int create_impl(const void* gguf, size_t len, const t5h_config* cfg, int hip_dev
                                     cfg->relative_attention_max_distance);
       for (int h = 0; h < H; h++) lut[(size_t)h * span + dlt + lutw] = tab[b * H + h];
     }
-    // Distance from which the bucket no longer changes (in either direction), so the bias is
-    // the LUT's end value: the attention kernel skips the bias reads for key tiles that far.
-    auto bucket = [cfg](int dlt) {
-      return rel_bucket(dlt < 0 ? (uint32_t)(-dlt) : 0u, dlt < 0 ? 0u : (uint32_t)dlt,
-                        cfg->relative_attention_num_buckets, cfg->relative_attention_max_distance);
-    };
-    int sat = lutw;
-    while (sat > 1 && bucket(sat - 1) == bucket(lutw) && bucket(-(sat - 1)) == bucket(-lutw)) sat--;
-    m->lut_sat = sat;
   }
   m->layers.resize(cfg->num_layers);
   for (int l = 0; l < cfg->num_layers; l++) {
