@@ -169,7 +169,8 @@ int t5h_q4k_q8k_matmul(int32_t hip_device, const uint8_t* w, int32_t N, const ui
 
 /* The attention work list the encoder uploads for a batch (cu_seqlens[batch + 1]) of `heads`
  * heads: items of 4 int32 (sequence start, length, first query, head), one per workgroup of
- * 128 queries of one (sequence, head), length 0 for the empty slots that pad the 8 per-XCD lists
+ * 64 queries (sequences of at most 128 tokens) or 128 queries (longer ones) of one (sequence,
+ * head), length 0 for the empty slots that pad the 8 per-XCD lists
  * (item i runs on XCD i % 8).  *n_items receives the item count; T5H_ERR_INVALID when it
  * exceeds cap.  Host only, no device needed. */
 int t5h_attention_work(const int32_t* cu_seqlens, int32_t batch, int32_t heads, int32_t* items, int32_t cap,

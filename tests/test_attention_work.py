@@ -7,7 +7,11 @@ import pytest
 
 from witchcraft_amd.encoder import attention_work
 
-QT = 128  # queries per workgroup
+QT, SMALL_L = 128, 128  # queries per workgroup; sequences up to SMALL_L tokens take 64
+
+
+def item_queries(L):
+    return 64 if L <= SMALL_L else QT
 
 
 def _check(cu, heads, max_len=2048):
@@ -18,7 +22,7 @@ def _check(cu, heads, max_len=2048):
     B = len(cu) - 1
     # every (sequence, head, query tile) exactly once
     want = {(int(cu[b]), int(cu[b + 1] - cu[b]), q, h)
-            for b in range(B) for h in range(heads) for q in range(0, int(cu[b + 1] - cu[b]), QT)}
+            for b in range(B) for h in range(heads) for q in range(0, int(cu[b + 1] - cu[b]), item_queries(int(cu[b + 1] - cu[b])))}
     real = [tuple(int(v) for v in it) for it in items if it[1] > 0]
     assert len(real) == len(set(real)) == len(want)
     assert set(real) == want
@@ -43,9 +47,9 @@ def _check(cu, heads, max_len=2048):
         slots_ = [s for _, s, _ in locs]
         assert slots_ == list(range(slots_[0], slots_[0] + len(slots_))), key
         assert [q for _, _, q in locs] == sorted(q for _, _, q in locs)
-    # within the workspace's reservation: heads * (ceil(T / 64) + B) + 8 * (ceil(max_len / 64) + 1)
+    # within the workspace's reservation: heads * (ceil(T / 64) + B) + 8 * (max(2, items(max_len)) + 1)
     T = int(cu[-1])
-    assert n <= heads * ((T + QT - 1) // QT + B) + 8 * ((max_len + QT - 1) // QT + 1)
+    assert n <= heads * ((T + 63) // 64 + B) + 8 * (max(2, (max_len + QT - 1) // QT) + 1)
     return items
 
 
@@ -64,6 +68,8 @@ def test_edge_batches():
     _check(np.array([0, 32], np.int32), 12)       # the query regime
     _check(np.array([0, 0, 5, 5, 70], np.int32), 3)  # empty sequences
     _check(np.array([0, 2048], np.int32), 1)
+    _check(np.array([0, 64, 129, 193, 321], np.int32), 12)  # either side of the 64-query items
+    _check(np.array([0, 65, 193], np.int32), 2)
     assert len(attention_work(np.array([0], np.int32), 12)) == 0  # no sequences
 
 

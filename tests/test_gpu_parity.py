@@ -115,11 +115,12 @@ def test_small_model_ragged_batch(small):
 
 
 def test_small_model_ragged_batch_tile_boundaries(small):
-    """Lengths at the attention's key-tile (64), half-tile (32) and 128-query tile edges: one-tile
-    sequences, last tiles with one or two valid 32-key halves, and second query tiles of 1 to
-    128 queries."""
+    """Lengths at the attention's key-tile (64), half-tile (32) and query-item edges: sequences of
+    up to 128 tokens in 64-query items over one or two key tiles (a second item of 1 to 64
+    queries), longer ones in 128-query items whose last tile holds one or two valid 32-key
+    halves, and second items of 1 to 128 queries."""
     cfg, _, gpu, ora = small
-    lens = [66, 96, 97, 127, 128, 129, 160, 161, 191, 192, 193, 255, 256, 32, 33]
+    lens = [64, 65, 66, 80, 96, 97, 127, 128, 129, 160, 161, 191, 192, 193, 255, 256, 32, 33, 1, 17]
     cu = np.zeros(len(lens) + 1, np.int32)
     cu[1:] = np.cumsum(lens)
     ids = np.random.default_rng(4).integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)

@@ -122,8 +122,16 @@ __host__ __device__ __forceinline__ float norm_operand_scale(float inv) {
   return s;
 }
 
-// Queries per attention workgroup (one work list item): 4 waves x 32.
+// Queries per attention work list item (one workgroup): 4 waves x 32 for sequences longer than
+// ATTN_SMALL_L tokens, 4 waves x 16 up to that length.  The split depends on the sequence's own
+// length only.
 constexpr int ATTN_QT = 128;
+constexpr int ATTN_SMALL_L = 128;
+__host__ __device__ __forceinline__ int attn_item_queries(int L) { return L <= ATTN_SMALL_L ? 64 : ATTN_QT; }
+__host__ __device__ __forceinline__ int attn_items(int L) {
+  const int q = attn_item_queries(L);
+  return (L + q - 1) / q;
+}
 
 struct AttnArgs {
   const _Float16* qkv;  // [3][H][tpad][dkv]

@@ -13,8 +13,8 @@
 // Keys are streamed in tiles of 64 through a three-deep LDS ring with an online softmax.  The
 // tiles travel global -> LDS without registers (global_load_lds_dwordx4): K and V rows as they
 // lie in memory, 128 B per key, and the bias values a tile needs (by j - i).  A tile's loads
-// are issued two tiles ahead; one barrier per tile.  A sequence of at most 64 tokens takes a
-// one-tile path with 16-query waves instead (short_sequence).
+// are issued two tiles ahead; one barrier per tile.  A sequence of at most 128 tokens takes a
+// path with 64-query work items and 16-query waves instead (small_sequence).
 //
 // The score block is computed transposed, S^T = K . Q^T (32 keys x 32 queries per MFMA), so
 // that the accumulator layout (lane = query column; lane half h holds keys 8a + 4h + b) is, four
@@ -37,7 +37,7 @@ constexpr int DK = 64;          // head dim (d_kv)
 constexpr int BSN = 64 * NWV;   // bias values staged per tile (QT + KT - 1 of them are read)
 constexpr int LOADS = 5;        // global -> LDS loads per wave per tile: 2 K, 2 V, 1 bias
 constexpr float LOG2E = 1.4426950408889634f;
-static_assert(NWV == 4 && 16 * NWV == KT && BSN >= QT + KT, "tile shape");
+static_assert(NWV == 4 && 16 * NWV == KT && BSN >= QT + KT && BSN >= 256 && ATTN_SMALL_L == 2 * KT, "tile shape");
 
 typedef short s4v __attribute__((ext_vector_type(4)));
 
@@ -229,25 +229,26 @@ __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* V
   }
 }
 
-// A sequence of at most 64 tokens: one key tile and at most 64 queries, taken by the four waves
-// as 16 queries each on v_mfma_f32_16x16x32_f16 -- half the chain of dependent work per wave of
-// the 32-query path, which is what bounds such short launches -- and with no running max: the
-// tile's own max is the reference.  Whether a sequence takes this path depends on its length
-// only, so its result does not depend on the batch around it.
+// A sequence of at most 128 tokens: one or two key tiles, whose work items hold 64 queries
+// (attn_item_queries), taken by the four waves as 16 queries each on v_mfma_f32_16x16x32_f16 --
+// half the chain of dependent work per wave of the 32-query path, which is what bounds such
+// short launches -- and with no running max: the scores of every key are taken before the
+// softmax, whose reference is their max.  Whether a sequence takes this path depends on its
+// length only, so its result does not depend on the batch around it.
 //
 // Layouts of the 16x16x32 product: A lane l = row l % 16, K 8 (l / 16) .. +7; B lane l = column
 // l % 16, the same K; D lane l register i = row 4 (l / 16) + i, column l % 16.  S^T = K . Q^T in
 // key blocks of 16, so lane (lr, lg) = (l % 16, l / 16) holds query lr against keys
 // 16 kb + 4 lg + i; the P^T operand of key step ks (32 keys) is then registers 0..3 of blocks
 // 2 ks and 2 ks + 1, keys {32 ks + 4 lg + i, 32 ks + 16 + 4 lg + i}, and the V^T operand is read
-// in that key order.
+// in that key order.  Key block kb lies in tile kb / 4 (Ks[kb / 4], Vs[kb / 4]).
 template <int NKB>
-__device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* Vs, const float* Bs, const h8 (&qf)[2],
-                                           int L, int s0, int hd, int qi, const AttnArgs& p) {
+__device__ __forceinline__ void small_tiles(const Slot& S0, const Slot& S1, const float* Bs, const h8 (&qf)[2], int L, int q0, int s0, int hd,
+                                            int qi, const AttnArgs& p) {
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4, wave = threadIdx.x >> 6;
   constexpr int NKS = (NKB + 1) / 2;  // 32-key P.V steps holding keys < L
-  // bias of (key j, query i) staged at j - i + 63
-  const int bofs = 63 - 16 * wave - lr + 4 * lg;
+  // bias of (key j, query i) staged at j - i + 127
+  const int bofs = 127 - q0 - 16 * wave - lr + 4 * lg;
   f4 s[2 * NKS];
 #pragma unroll
   for (int kb = 0; kb < 2 * NKS; kb++)
@@ -257,7 +258,7 @@ __device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* V
   for (int ds = 0; ds < 2; ds++)
 #pragma unroll
     for (int kb = 0; kb < NKB; kb++) {
-      const h8 a = *reinterpret_cast<const h8*>(&Ks[swz<ROT_8>(16 * kb + lr, 32 * ds + 8 * lg)]);
+      const h8 a = *reinterpret_cast<const h8*>(&(kb >> 2 ? S1 : S0).k[swz<ROT_8>(16 * (kb & 3) + lr, 32 * ds + 8 * lg)]);
       s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ds], s[kb], 0, 0, 0);
     }
   float mx = -INFINITY;
@@ -285,8 +286,9 @@ __device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* V
   }
   l = sum_xor32(sum_xor16(l));
   // O^T[d][query] = V^T[d][keys] . P^T[keys][query]: lane (n, g) = (l % 16, l / 16) of 16-lane group g
-  // reads rows 32 ks + 4 g + i / 4 (+ 16), dims 16 db + 4 (i % 4); the transposing read returns
-  // V[32 ks + 4 g + r][16 db + n] (and 16 rows on), the keys of its P^T slots.
+  // reads rows 32 ks + 4 g + i / 4 (+ 16) of the step's tile, dims 16 db + 4 (i % 4); the
+  // transposing read returns V[32 ks + 4 g + r][16 db + n] (and 16 rows on), the keys of its
+  // P^T slots.
   typedef __attribute__((address_space(3))) s4v lds_s4;
   f4 o[4];
 #pragma unroll
@@ -294,9 +296,10 @@ __device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* V
     o[db] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) {
-      const int row = 32 * ks + 4 * lg + (lr >> 2), col = 16 * db + 4 * (lr & 3);
-      const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vs + swz<ROT_8>(row, col)));
-      const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vs + swz<ROT_8>(row + 16, col)));
+      const _Float16* Vt = (ks >> 1 ? S1 : S0).v;
+      const int row = 32 * (ks & 1) + 4 * lg + (lr >> 2), col = 16 * db + 4 * (lr & 3);
+      const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vt + swz<ROT_8>(row, col)));
+      const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(Vt + swz<ROT_8>(row + 16, col)));
       h8 v;
       __builtin_memcpy(&v, &lo, 8);
       __builtin_memcpy(reinterpret_cast<char*>(&v) + 8, &hi, 8);
@@ -314,18 +317,24 @@ __device__ __forceinline__ void short_tile(const _Float16* Ks, const _Float16* V
   }
 }
 
-__device__ __forceinline__ void short_sequence(const AttnArgs& p, Slot& sl, int s0, int L, int hd, int wave, int lane) {
+// The loads of a sequence of at most 128 tokens: its one or two K and V tiles (rows past L
+// repeat the last row) and the bias of distances -127 .. 128, all in one round trip, then the
+// 64 queries from q0 (0 or 64).
+__device__ __forceinline__ void small_sequence(const AttnArgs& p, Slot& S0, Slot& S1, int s0, int L, int q0, int hd, int wave, int lane) {
   const size_t head_stride = (size_t)p.tpad * DK;
   const _Float16* Q = p.qkv + ((size_t)0 * p.heads + hd) * head_stride + (size_t)s0 * DK;
   const _Float16* Kg = p.qkv + ((size_t)1 * p.heads + hd) * head_stride + (size_t)s0 * DK;
   const _Float16* Vg = p.qkv + ((size_t)2 * p.heads + hd) * head_stride + (size_t)s0 * DK;
   const float* lut = p.lut + (size_t)hd * (2 * p.lutw + 1) + p.lutw;
-  // the tile (rows past L repeat the last row) and the bias of distances -63 .. 64
-  dma_tile<ROT_8>(Kg, L, sl.k, wave, lane);
-  dma_tile<ROT_8>(Vg, L, sl.v, wave, lane);
-  if (wave < 2) lds_load4(lut + (64 * wave - 63 + lane), lds_offset(sl.b + 64 * wave));
-  const int lr = lane & 15, lg = lane >> 4, qi = 16 * wave + lr;
-  const bool active = 16 * wave < L;  // wave-uniform
+  const int ntile = (L + KT - 1) / KT;  // 1 or 2
+  for (int t = 0; t < ntile; t++) {
+    Slot& d = t ? S1 : S0;
+    dma_tile<ROT_8>(Kg + (size_t)t * KT * DK, L - t * KT, d.k, wave, lane);
+    dma_tile<ROT_8>(Vg + (size_t)t * KT * DK, L - t * KT, d.v, wave, lane);
+  }
+  lds_load4(lut + (64 * wave - 127 + lane), lds_offset(S0.b + 64 * wave));
+  const int lr = lane & 15, lg = lane >> 4, qi = q0 + 16 * wave + lr;
+  const bool active = q0 + 16 * wave < L;  // wave-uniform
   h8 qf[2];
   if (active) {
     qf[0] = *reinterpret_cast<const h8*>(Q + (size_t)qi * DK + 8 * lg);
@@ -334,10 +343,14 @@ __device__ __forceinline__ void short_sequence(const AttnArgs& p, Slot& sl, int 
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (!active) return;
   switch ((L + 15) >> 4) {
-    case 1: short_tile<1>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
-    case 2: short_tile<2>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
-    case 3: short_tile<3>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
-    default: short_tile<4>(sl.k, sl.v, sl.b, qf, L, s0, hd, qi, p); break;
+    case 1: small_tiles<1>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 2: small_tiles<2>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 3: small_tiles<3>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 4: small_tiles<4>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 5: small_tiles<5>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 6: small_tiles<6>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    case 7: small_tiles<7>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
+    default: small_tiles<8>(S0, S1, S0.b, qf, L, q0, s0, hd, qi, p); break;
   }
 }
 
@@ -348,8 +361,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
   const int4 wk = p.work[blockIdx.x];
   const int s0 = wk.x, L = wk.y, q0 = wk.z, hd = wk.w;
   if (L == 0) return;  // an empty slot of the work list (the whole workgroup)
-  if (L <= KT) {        // one key tile, one query tile (uniform across the workgroup)
-    short_sequence(p, S0, s0, L, hd, wave, lane);
+  if (L <= ATTN_SMALL_L) {  // one or two key tiles, 64-query items (uniform across the workgroup)
+    small_sequence(p, S0, S1, s0, L, q0, hd, wave, lane);
     return;
   }
   const int l32 = lane & 31, h = lane >> 5;

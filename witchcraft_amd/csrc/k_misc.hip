@@ -261,9 +261,9 @@ __global__ void f32_to_f16_kernel(const float* __restrict__ x, _Float16* __restr
 __global__ __launch_bounds__(256) void work_list_kernel(t5k::WorkChunk c, int4* __restrict__ work) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= c.n) return;
-  const int L = c.len[i], n = L ? (L + ATTN_QT - 1) / ATTN_QT : c.start[i];
+  const int L = c.len[i], n = L ? attn_items(L) : c.start[i];
   for (int q = 0; q < n; q++)
-    work[c.pos[i] + 8 * q] = L ? make_int4(c.start[i], L, q * ATTN_QT, c.head[i]) : make_int4(0, 0, 0, 0);
+    work[c.pos[i] + 8 * q] = L ? make_int4(c.start[i], L, q * attn_item_queries(L), c.head[i]) : make_int4(0, 0, 0, 0);
 }
 
 }  // namespace

@@ -755,7 +755,8 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
   return T5H_OK;
 }
 
-// Attention work plan.  One workgroup per (sequence, head, ATTN_QT queries); workgroup b runs on
+// Attention work plan.  One workgroup per (sequence, head, attn_item_queries(L) queries: 64 up
+// to ATTN_SMALL_L tokens, ATTN_QT above); workgroup b runs on
 // XCD b % 8 (workgroups are dealt round-robin), so the list is laid out as 8 interleaved
 // per-XCD lists.  All query tiles of one (sequence, head) go to one XCD, one after another, so
 // that XCD's L2 holds the group's keys and values while its query tiles stream them (2048
@@ -763,12 +764,14 @@ int gemm(t5h_model* m, int kind, int epi, const Linear& W, const Linear* W1, con
 // and each goes to the XCD with the least work (query tiles x key tiles) among those whose
 // list stays within ceil(items / 8) + the longest group, which bounds the padding: the lists
 // are padded to the longest one with empty items (length 0), which exit at once.
-int attn_tiles(int L) { return (L + ATTN_QT - 1) / ATTN_QT; }
+int attn_tiles(int L) { return attn_items(L); }
 
 // Upper bound of the work list length (items incl. padding) for T tokens in B sequences of at
 // most max_len tokens.
 int attn_work_cap(int heads, int max_seq_len, int T, int B) {
-  return heads * ((T + ATTN_QT - 1) / ATTN_QT + B) + 8 * (attn_tiles(max_seq_len) + 1);
+  // items of at least 64 queries: ceil(L / 64) <= L / 64 + 1 per sequence; at most 2 for
+  // L <= ATTN_SMALL_L, ceil(L / ATTN_QT) above
+  return heads * ((T + 63) / 64 + B) + 8 * (std::max(2, attn_tiles(max_seq_len)) + 1);
 }
 int attn_work_cap(const t5h_model* m, int T, int B) { return attn_work_cap(m->cfg.num_heads, m->cfg.max_seq_len, T, B); }
 
@@ -813,7 +816,8 @@ int write_attention_work(int H, const int32_t* cu, const std::vector<int>& order
   const int slots = plan_attention(H, cu, order, xlen, [](const AttnGroup&) {});
   if ((size_t)8 * slots > cap) return -1;
   plan_attention(H, cu, order, xlen, [&](const AttnGroup& g) {
-    for (int q = 0; q < attn_tiles(g.len); q++) out[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * ATTN_QT, g.head);
+    for (int q = 0; q < attn_tiles(g.len); q++)
+      out[(size_t)(g.slot0 + q) * 8 + g.xcd] = make_int4(g.start, g.len, q * attn_item_queries(g.len), g.head);
   });
   for (int x = 0; x < 8; x++)
     for (int q = xlen[x]; q < slots; q++) out[(size_t)q * 8 + x] = make_int4(0, 0, 0, 0);

@@ -222,8 +222,9 @@ class T5ModelBuilder:
 
 def attention_work(cu_seqlens: np.ndarray, heads: int) -> np.ndarray:
     """The attention work list the encoder uploads for a batch: [n, 4] int32 items (sequence
-    start, length, first query, head), one per 64-query workgroup, length 0 for the padding of
-    the 8 per-XCD lists; item i runs on XCD i % 8.  Host only."""
+    start, length, first query, head), one per workgroup of 64 queries (sequences of at most 128
+    tokens) or 128 (longer ones), length 0 for the padding of the 8 per-XCD lists; item i runs
+    on XCD i % 8.  Host only."""
     cu = np.ascontiguousarray(cu_seqlens, np.int32).reshape(-1)
     B = cu.size - 1
     cap = heads * (int(cu[-1]) // 64 + 2 * B + 8) + 8 * 64 + 64 if B > 0 else 64
