@@ -360,18 +360,24 @@ __device__ __forceinline__ void math_hybrid(const GemmArgs& p, int m0, _Float16 
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* hi = reinterpret_cast<const uint8_t*>(Bs[kt & 1]);
       const uint8_t* lo = hi + BN * 64;
+      // every fragment of the step is requested before the first MFMA, so the LDS latency is
+      // paid once per step rather than once per row block
+      v4i wh[NB], wl[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; nb++) {
-        const v4i wh = *reinterpret_cast<const v4i*>(hi + foff[nb]);
-        const v4i wl = *reinterpret_cast<const v4i*>(lo + foff[nb]);
+        wh[nb] = *reinterpret_cast<const v4i*>(hi + foff[nb]);
+        wl[nb] = *reinterpret_cast<const v4i*>(lo + foff[nb]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
           const v4i x = __builtin_bit_cast(v4i, a[u % S][mb]);
-          acc_hi[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh, x, u == 0 ? izero : acc_hi[mb][nb], 0, 0, 0);
-          acc_lo[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl, x, u == 0 ? izero : acc_lo[mb][nb], 0, 0, 0);
+          acc_hi[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wh[nb], x, u == 0 ? izero : acc_hi[mb][nb], 0, 0, 0);
+          acc_lo[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wl[nb], x, u == 0 ? izero : acc_lo[mb][nb], 0, 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_sched_barrier(0);
       if (u == 3) {
         // block b's sums for the fold waves: lane holds rows 16nb + 4lg + i of token 16mb + lr
 #pragma unroll
