@@ -869,9 +869,12 @@ def summarize(args) -> None:
         if "FETCH_SIZE" in v and "WRITE_SIZE" in v and scale:
             traffic[c] = {"fetch": v["FETCH_SIZE"] * 1024 * scale.get("FETCH_SIZE", 1.0),
                           "write": v["WRITE_SIZE"] * 1024 * scale.get("WRITE_SIZE", 1.0)}
-        if "SQ_INSTS_VALU_MFMA_F16" in v:
-            # the counter counts instructions: attention runs 32x32x16 products, the GEMMs 16x16x32
-            v["mfma_flop_executed"] = v["SQ_INSTS_VALU_MFMA_F16"] * (32 * 32 * 16 if c == "attention" else 16 * 16 * 32) * 2
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in v:
+            # f16 MFMA work in units of 512 FLOP, whatever the instruction shape
+            v["mfma_flop_executed"] = v["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512
+        elif "SQ_INSTS_VALU_MFMA_F16" in v and c != "attention":
+            # an instruction count: the GEMMs run only 16x16x32 products (attention mixes shapes)
+            v["mfma_flop_executed"] = v["SQ_INSTS_VALU_MFMA_F16"] * 16 * 16 * 32 * 2
         if "SQ_VALU_MFMA_BUSY_CYCLES" in v and "GRBM_GUI_ACTIVE" in v:
             v["mfma_busy_frac"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * v["GRBM_GUI_ACTIVE"] / 8)
     summary["scale"] = scale
