@@ -148,6 +148,28 @@ def test_small_model_random_ragged_batches(small, seed):
         assert np.array_equal(out2[cu2[j]:cu2[j + 1]].view(np.uint32), out[cu[b]:cu[b + 1]].view(np.uint32)), (b, lens[b])
 
 
+def test_small_model_many_short_sequences(small):
+    """A call of 3,000 sequences: 2,000 of 1 to 3 tokens and 1,000 of 65 to 128 tokens (two
+    64-query attention items each), shuffled. The attention work list then holds far more items
+    than tokens / 128, as its reserved capacity must allow. A sample of sequences is checked
+    against the oracle, and every sequence is bit-identical to its own call."""
+    cfg, _, gpu, ora = small
+    rng = np.random.default_rng(31)
+    lens = np.concatenate([rng.integers(1, 4, size=2000), rng.integers(65, 129, size=1000)])
+    lens = lens[rng.permutation(lens.size)]
+    cu = np.zeros(lens.size + 1, np.int32)
+    cu[1:] = np.cumsum(lens)
+    ids = rng.integers(1, cfg["vocab_size"], size=int(cu[-1])).astype(np.uint32)
+    out, _ = gpu.encode_packed(ids, cu)
+    assert np.isfinite(out).all()
+    for b in list(rng.choice(lens.size, 12, replace=False)) + [int(np.argmax(lens)), int(np.argmin(lens))]:
+        s, e = int(cu[b]), int(cu[b + 1])
+        assert cos_rows(out[s:e], ora.forward(ids[s:e])).min() >= COS_MIN, (b, e - s)
+        if e - s > 64:  # above the GEMV path, whose rounding differs from the batched GEMMs
+            alone, _ = gpu.encode_packed(ids[s:e], np.array([0, e - s], np.int32))
+            assert np.array_equal(alone.view(np.uint32), out[s:e].view(np.uint32)), (b, e - s)
+
+
 def test_small_model_ragged_batch_past_four_key_tiles(small):
     """5 to 8 key tiles of 64 per sequence: the attention's three-slot load ring wraps more than
     once, through both the loop body and the steps after it."""
