@@ -74,14 +74,18 @@ __device__ __forceinline__ int swz(int row, int col) {
 // vmcnt before the barrier that publishes the tile; the "memory" clobbers keep every LDS
 // access on its side of these statements.  M0 holds the wave's LDS destination; the 16-byte
 // form writes lane l's 16 bytes at M0 + 16 l, the 4-byte form lane l's 4 bytes at M0 + 4 l.
+// The source address is a wave-uniform base (an SGPR pair) plus the lane's 32-bit byte offset,
+// so a tile's loads cost no 64-bit address arithmetic per lane.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
-__device__ __forceinline__ void lds_load16(const void* src, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+__device__ __forceinline__ void lds_load16(const void* base, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+               : "memory", "m0");
 }
-__device__ __forceinline__ void lds_load4(const void* src, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+__device__ __forceinline__ void lds_load4(const void* base, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+               : "memory", "m0");
 }
 
 // Global -> LDS copy of one 64-row tile by this wave's 16 rows: LDS slot l of an instruction
@@ -96,7 +100,7 @@ __device__ __forceinline__ void dma_tile(const _Float16* src, int nrows, _Float1
     const int row = 16 * wave + 8 * j + (lane >> 3);
     const int chunk = (lane ^ rot<R>(row)) & 7;
     const int srow = row < nrows ? row : nrows - 1;
-    lds_load16(src + (size_t)srow * DK + chunk * 8, lds_offset(dst + (16 * wave + 8 * j) * DK));
+    lds_load16(src, (uint32_t)(srow * (DK * 2) + chunk * 16), lds_offset(dst + (16 * wave + 8 * j) * DK));
   }
 }
 
@@ -332,7 +336,7 @@ __device__ __forceinline__ void small_sequence(const AttnArgs& p, Slot& S0, Slot
     dma_tile<ROT_8>(Kg + (size_t)t * KT * DK, L - t * KT, d.k, wave, lane);
     dma_tile<ROT_8>(Vg + (size_t)t * KT * DK, L - t * KT, d.v, wave, lane);
   }
-  lds_load4(lut + (64 * wave - 127 + lane), lds_offset(S0.b + 64 * wave));
+  lds_load4(lut + (64 * wave - 127), 4u * lane, lds_offset(S0.b + 64 * wave));
   const int lr = lane & 15, lg = lane >> 4, qi = q0 + 16 * wave + lr;
   const bool active = q0 + 16 * wave < L;  // wave-uniform
   h8 qf[2];
@@ -385,7 +389,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3))) v
   auto load_tile = [&](int k0, _Float16* Kd, _Float16* Vd, float* Bd) __attribute__((always_inline)) {
     dma_tile<ROT_K>(Kg + (size_t)k0 * DK, L - k0, Kd, wave, lane);
     dma_tile<ROT_V>(Vg + (size_t)k0 * DK, L - k0, Vd, wave, lane);
-    lds_load4(lut + (k0 - q0 - (QT - 1) + 64 * wave + lane), lds_offset(Bd + 64 * wave));
+    lds_load4(lut + (k0 - q0 - (QT - 1) + 64 * wave), 4u * lane, lds_offset(Bd + 64 * wave));
   };
   static_assert(LOADS == 5, "the wait below counts five loads per tile");
 
