@@ -164,12 +164,19 @@ __device__ __forceinline__ void attn_tile(const _Float16* Ksb, const _Float16* V
   asm volatile("" : "+v"(bofs), "+v"(lo.k[0]), "+v"(lo.k[1]), "+v"(lo.k[2]), "+v"(lo.k[3]), "+v"(lo.v[0]),
                "+v"(lo.v[1]));
   // S^T[key][query] + bias: register r of half kb holds key 32 kb + 8 (r / 4) + 4 h + r % 4.
-  // The accumulators start from the bias, so the matrix core does the add.
+  // The accumulators start from the bias, so the matrix core does the add.  The lane's bias
+  // address is formed once per tile and kept opaque, so its 32 reads (all within 60 floats)
+  // pair up as ds_read2_b32 with immediate offsets from that one register; a slot base too large
+  // for those offsets would otherwise be added per pair.
+  typedef const __attribute__((address_space(3))) float lds_f;
+  uint32_t baddr = lds_offset(Bsb) + 4u * (uint32_t)bofs;
+  asm volatile("" : "+v"(baddr));
+  lds_f* bsrc = (lds_f*)(uintptr_t)baddr;
   f16v s[NS];
 #pragma unroll
   for (int kb = 0; kb < NS; kb++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) s[kb][r] = Bsb[bofs + 32 * kb + 8 * (r >> 2) + (r & 3)];
+    for (int r = 0; r < 16; r++) s[kb][r] = bsrc[32 * kb + 8 * (r >> 2) + (r & 3)];
   // every LDS operand of the tile is read before the products that use it: the K operands
   // ahead of the score products, the V^T operands ahead of the softmax, whose VALU work covers
   // their latency
