@@ -487,7 +487,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
   constexpr int PB = 4;
   using R = BRaw<WF, NP, BN>;
   const int nkt = p.K / BK;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   // waves [0, MW) compute, waves [MW, 2MW) produce; wave w runs on SIMD w % 4
 
   if (wave >= MW) {
@@ -540,9 +540,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
   const int lr = lane & 15, lg = lane >> 4;
   // operand blocks of this wave's MB row groups: block (rb, kb) at ((rb * K/32) + kb) * 512
   const size_t kblk = p.K / 32;
+  // wave-uniform block bases plus the lane's 16 bytes: the loads take the base from SGPRs
   const _Float16* ablk[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; mb++) ablk[mb] = p.A + ((size_t)((m0 + wave * 16 * MB) / 16 + mb) * kblk) * 512 + lane * 8;
+  for (int mb = 0; mb < MB; mb++) ablk[mb] = p.A + ((size_t)((m0 + wave * 16 * MB) / 16 + mb) * kblk) * 512;
+  uint32_t alane = 16u * lane;
 
   f4 acc[MB][NB];
 #pragma unroll
@@ -559,9 +561,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int m0, int n0, _Fl
   // A ring: step j in register stage j % S, loaded S-1 steps before it is used.
   uint4 a[S][MB][2];
 #define LOAD_A(st, kt)                                                                      \
+  asm volatile("" : "+v"(alane));                                                            \
   _Pragma("unroll") for (int mb = 0; mb < MB; mb++) {                                        \
-    a[st][mb][0] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt)) * 512);     \
-    a[st][mb][1] = *reinterpret_cast<const uint4*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512); \
+    a[st][mb][0] = *reinterpret_cast<const uint4*>(                                          \
+        reinterpret_cast<const char*>(ablk[mb] + (size_t)(2 * (kt)) * 512) + alane);           \
+    a[st][mb][1] = *reinterpret_cast<const uint4*>(                                          \
+        reinterpret_cast<const char*>(ablk[mb] + (size_t)(2 * (kt) + 1) * 512) + alane);       \
   }
 #pragma unroll
   for (int i = 0; i < S - 1; i++) {
