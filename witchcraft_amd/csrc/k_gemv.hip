@@ -28,20 +28,26 @@
 
 namespace {
 
-// Raw bytes of one 64-wide K chunk of weight row n for MFMA A-operand lane group lg:
+// Raw bytes of one 64-wide K chunk of weight row n0 + lr for MFMA A-operand lane group lg:
 // Q4_K: r0 = block header (d, dmin, scales), r1.xy = nibble bytes qs[32c + 8lg .. +7];
-// f16: r0 = W[n][k + 8lg .. +7], r1 = W[n][k + 32 + 8lg .. +7].
+// f16: r0 = W[n][k + 8lg .. +7], r1 = W[n][k + 32 + 8lg .. +7].  n0 and k are wave-uniform, so
+// each load is an SGPR base plus the lane's 32-bit byte offset (no per-lane 64-bit address math
+// ahead of the launch's one memory round trip).
 template <int WF>
-__device__ __forceinline__ void wload(const void* W, int K, int n, int k, int lg, uint4& r0, uint4& r1) {
+__device__ __forceinline__ void wload(const void* W, int K, int n0, int lr, int k, int lg, uint4& r0, uint4& r1) {
   if constexpr (WF == WF_Q4K) {
-    const uint8_t* blk = (const uint8_t*)W + ((size_t)n * (K / QK_K) + k / QK_K) * Q4K_BYTES;
-    r0 = *reinterpret_cast<const uint4*>(blk);
-    const uint2 q = *reinterpret_cast<const uint2*>(blk + 16 + 32 * ((k % QK_K) / 64) + 8 * lg);
+    const uint8_t* blk = (const uint8_t*)W + ((size_t)n0 * (K / QK_K) + k / QK_K) * Q4K_BYTES;
+    uint32_t ro = (uint32_t)(lr * (K / QK_K) * Q4K_BYTES);
+    asm volatile("" : "+v"(ro));  // an opaque 32-bit lane offset: the saddr form, not a 64-bit VGPR address
+    r0 = *reinterpret_cast<const uint4*>(blk + ro);
+    const uint2 q = *reinterpret_cast<const uint2*>(blk + 16 + 32 * ((k % QK_K) / 64) + ro + 8u * lg);
     r1 = make_uint4(q.x, q.y, 0u, 0u);
   } else {
-    const _Float16* row = (const _Float16*)W + (size_t)n * K + k + 8 * lg;
-    r0 = *reinterpret_cast<const uint4*>(row);
-    r1 = *reinterpret_cast<const uint4*>(row + 32);
+    const char* row = (const char*)((const _Float16*)W + (size_t)n0 * K + k);
+    uint32_t ro = (uint32_t)(lr * K * 2 + 16 * lg);
+    asm volatile("" : "+v"(ro));
+    r0 = *reinterpret_cast<const uint4*>(row + ro);
+    r1 = *reinterpret_cast<const uint4*>(row + 64 + ro);
   }
 }
 
@@ -82,14 +88,17 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
   extern __shared__ f4 red[];
   __shared__ float rinv[NORM ? MT * 16 : 1];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nw = blockDim.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int tb0 = blockIdx.y * MT;  // first 16-token block of this workgroup
   const int kw = p.K / nw, kbeg = wave * kw, nch = kw / 64;
   const size_t kblk = p.K / 32;
-  const _Float16* xa = p.A + lane * 8;  // operand block (mt, kb) at (mt * K/32 + kb) * 512
+  // operand block (mt, kb) at (mt * K/32 + kb) * 512 halves; lane l reads its 16 bytes at 16 l
+  const _Float16* xa = p.A;
+  uint32_t xl = 16u * lane;
+  asm volatile("" : "+v"(xl));
   const void* Wg[2] = {p.W0, p.W1};
 
   uint4 raw[GROUP][G][2];
@@ -103,7 +112,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
     if ((c0) + c < nch) {                                                                      \
       const int k = kbeg + 64 * ((c0) + c);                                                    \
       _Pragma("unroll") for (int g = 0; g < G; g++)                                            \
-          wload<WF>(Wg[g], p.K, n0 + lr, k, lg, raw[c][g][0], raw[c][g][1]);                  \
+          wload<WF>(Wg[g], p.K, n0, lr, k, lg, raw[c][g][0], raw[c][g][1]);                   \
     }                                                                                          \
   }
 #define GEMV_LOAD_X(c0)                                                                          \
@@ -125,7 +134,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemmArgs p) {
           }                                                                                    \
         } else {                                                                               \
           _Pragma("unroll") for (int mt = 0; mt < MT; mt++)                                    \
-              xr[c][s][mt] = *reinterpret_cast<const uint4*>(xa + ((size_t)(tb0 + mt) * kblk + k / 32 + s) * 512); \
+              xr[c][s][mt] = *reinterpret_cast<const uint4*>(                                  \
+                  reinterpret_cast<const char*>(xa + ((size_t)(tb0 + mt) * kblk + k / 32 + s) * 512) + xl); \
         }                                                                                      \
       }                                                                                        \
     }                                                                                          \
